@@ -1,0 +1,256 @@
+"""Benchmark of the whisper.rs attention path on one MI355X.
+
+Headline workload (``value``): whisper-large-v3 encoder self-attention,
+16 windows x 20 heads x 1500 frames x d_head 64, bf16 Q/K/V ~ N(0, 0.5^2)
+with 13 outlier channels x8, f32 accumulate -- one step is one prefill launch
+over all 16 windows, inputs resident in HBM. FLOPs are 4*B*H*T^2*d (the
+reference's convention, crates/tensor/tests/bench_flash_attention_tiled.rs:214).
+
+Second figure of the same metric (``decode_cross``): whisper-large-v3
+cross-attention decode, beam 5 x 20 heads against 1500 f16 encoder K/V per
+layer, 32 layers resident, one launch per layer. Three utterances' caches
+(737 MB) are rotated so the 256 MB MALL cannot hold them; the launches are
+replayed from a HIP graph. Bytes are the unique K/V bytes (read once for all
+beams) plus f32 Q and O.
+
+cpu_baseline: the CPU oracle (a C restatement of the reference path) timed on
+this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "encoder attn TFLOP/s (%MFMA peak) + decode cross-attn GB/s (%HBM), large-v3"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+
+
+def _load_pkg():
+    pkg_dir = ROOT / "whisper.rs_amd"
+    spec = importlib.util.spec_from_file_location(
+        "wrs_amd", pkg_dir / "__init__.py", submodule_search_locations=[str(pkg_dir)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["wrs_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def bench_encoder(wrs, W, ctx, steps, warmup):
+    import torch
+    cfg = W.LARGE_ENCODER
+    log(f"encoder: generating {cfg.name}")
+    q, k, v = cfg.inputs()
+    qd, kd, vd = (torch.from_numpy(x).to(torch.bfloat16).cuda() for x in (q, k, v))
+    B, T, dm = cfg.batch, cfg.t, cfg.d_model
+    out = torch.empty((B, T, dm), dtype=torch.float32, device="cuda")
+    lay = wrs.token_major(T, dm, 64)
+
+    def step():
+        wrs.prefill(qd, kd, vd, out, batch=B, n_heads=cfg.n_heads, t_q=T, t_kv=T, d_head=64,
+                    q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+
+    log(f"encoder: warmup {warmup}")
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"encoder: timing {steps} steps")
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tflops = cfg.flops() / (ms * 1e-3) / 1e12
+    return cfg, ms, tflops, (q, k, v)
+
+
+def bench_decode(wrs, W, ctx, reps):
+    import torch
+    cfg = W.LARGE_CROSS_DECODE
+    U = 3  # utterances rotated: 3 x 245.76 MB of cross K/V > 256 MB MALL
+    log(f"decode: building {U} x {cfg.n_layers}-layer cross caches")
+    arenas = []
+    for u in range(U):
+        ar = wrs.KvArena(cfg.n_layers, 1, cfg.n_heads, 448, cfg.n_audio, ctx=ctx)
+        for layer in range(cfg.n_layers):
+            kk, vv = cfg.kv(layer)
+            ar.set_cross(layer, torch.from_numpy(kk).cuda(), torch.from_numpy(vv).cuda())
+        arenas.append(ar)
+    qs = torch.from_numpy(np.stack([cfg.q(layer) for layer in range(cfg.n_layers)])).cuda()
+    outs = torch.zeros((U, cfg.n_layers, cfg.beams, cfg.d_model), device="cuda")
+
+    def all_layers():
+        for u in range(U):
+            for layer in range(cfg.n_layers):
+                arenas[u].decode_cross(layer, qs[layer], outs[u, layer])
+
+    all_layers()  # sizes the scratch outside any capture
+    torch.cuda.synchronize()
+    eager = outs.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.use_torch_stream()
+        all_layers()
+    ctx.use_torch_stream()
+    outs.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(outs, eager):
+        raise RuntimeError("graph replay of the decode launches differs from eager")
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"decode: timing {reps} graph replays of {U * cfg.n_layers} launches")
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    n_launch = reps * U * cfg.n_layers
+    us = start.elapsed_time(end) * 1e3 / n_launch
+    gbs = cfg.bytes_per_layer() / (us * 1e-6) / 1e9
+    for ar in arenas:
+        ar.close()
+    return cfg, us, gbs
+
+
+def copy_bandwidth():
+    import torch
+    n = 1 << 28  # 1 GiB of f32
+    a = torch.empty(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(10):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / 10
+    return 2 * a.numel() * 4 / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline_encoder(cfg, qkv, threads):
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    q, k, v = (np.ascontiguousarray(x[0].reshape(-1)) for x in qkv)
+    out = np.zeros_like(q)
+    T, H, dm = cfg.t, cfg.n_heads, cfg.d_model
+    best = float("inf")
+    t_end = time.time() + 20.0
+    reps = 0
+    while reps < 5 and (reps < 2 or time.time() < t_end):
+        t0 = time.perf_counter()
+        orc.flash_attention_2(q, k, v, T, T, H, dm, False, out, n_threads=threads)
+        best = min(best, time.perf_counter() - t0)
+        reps += 1
+    flops = 4.0 * H * T * T * 64
+    return {"value": flops / best / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"1 of 16 windows (20 heads x 1500 x 1500), best of {reps}, "
+                      f"{best * 1e3:.1f} ms"}
+
+
+def cpu_baseline_decode(cfg):
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    kk, vv = cfg.kv(0)
+    k, v = np.ascontiguousarray(kk.ravel()), np.ascontiguousarray(vv.ravel())
+    q = cfg.q(0)
+    out = np.zeros(cfg.d_model, np.float32)
+    best = float("inf")
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for b in range(cfg.beams):  # the reference's per-slot loop (decoder.rs:689-724)
+            orc.single_token_mha_d64(np.ascontiguousarray(q[b]), k, v, cfg.n_audio, cfg.n_heads,
+                                     cfg.d_model, out)
+        best = min(best, time.perf_counter() - t0)
+    return {"value": cfg.bytes_per_layer() / best / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"1 layer, 5 beams read serially from f32 K/V, best of 5, "
+                      f"{best * 1e3:.2f} ms"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-reps", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the attention path shards across GPUs without exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    wrs = _load_pkg()
+    from wrs_amd import workloads as W
+    ctx = wrs.Context(0)
+    ctx.use_torch_stream()
+    props = torch.cuda.get_device_properties(0)
+
+    cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
+    dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
+    copy_gbs = copy_bandwidth()
+
+    threads = min(16, os.cpu_count() or 1)
+    cpu_enc = cpu_dec = None
+    if not args.no_cpu:
+        log(f"cpu baseline: oracle encoder window on {threads} threads")
+        cpu_enc = cpu_baseline_encoder(cfg, qkv, threads)
+        log("cpu baseline: oracle decode layer, 1 thread")
+        cpu_dec = cpu_baseline_decode(dcfg)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": cfg.name, "windows": cfg.batch, "heads": cfg.n_heads,
+                   "frames": cfg.t, "d_head": 64, "flops_per_step": cfg.flops()},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu_enc,
+        "decode_cross": {
+            "workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s",
+            "us_per_launch": round(us, 3), "launches_per_step": dcfg.n_layers,
+            "bytes_per_launch": dcfg.bytes_per_layer(), "dtype": "f16",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+            "cpu_baseline": cpu_dec,
+        },
+        "device": {"name": props.name, "cu": props.multi_processor_count,
+                   "copy_GBps": round(copy_gbs, 1)},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,186 @@
+/*
+ * wrs_attn.h -- C ABI of the MI355X (gfx950) attention path for whisper.rs.
+ *
+ * Drop-in replacement for the reference's Flash-Attention-2 path
+ * (crates/tensor/src/ops/attention.rs, crates/tensor/src/ops/softmax.rs,
+ * crates/whisper/src/decoder.rs:131-264 and :835-892). Every entry point
+ * returns an int status: 0 on success, a negative WRS_E* code otherwise, and
+ * never unwinds across the ABI. Where the reference panics on a shape
+ * assertion, the call returns WRS_EINVAL without touching any output; the
+ * feature crate maps that back to a panic so the reference contract holds.
+ *
+ * Threading: a wrs_attn_ctx owns one HIP stream and its scratch memory and is
+ * used by one thread at a time (one per WhisperState, like the reference's
+ * per-state workspaces); independent contexts may run concurrently.
+ * Host-slice entry points are synchronous. Device-resident entry points are
+ * asynchronous on the context's stream.
+ */
+#ifndef WRS_ATTN_H
+#define WRS_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define WRS_OK 0
+#define WRS_EINVAL (-1)      /* shape/argument violation (reference: assert! panic) */
+#define WRS_ENOMEM (-2)      /* device or host allocation failed */
+#define WRS_EHIP (-3)        /* HIP runtime error; see wrs_attn_last_error */
+#define WRS_EUNSUPPORTED (-4) /* valid for the reference, not handled on the GPU */
+#define WRS_ERANGE (-5)      /* layer/slot index or length outside the arena */
+
+/* Element types of device-resident tensors. */
+#define WRS_F32 0
+#define WRS_F16 1
+#define WRS_BF16 2
+
+typedef struct wrs_attn_ctx wrs_attn_ctx;
+typedef struct wrs_kv wrs_kv;
+
+/* Strides, in elements, of a [batch][head][token][d] view of a tensor.
+ * The reference's token-major rows [t][d_model] are
+ * {batch: T*d_model, head: d_head, row: d_model}; a fused QKV projection
+ * output [t][3*d_model] is the same with row = 3*d_model. */
+typedef struct wrs_layout {
+    int64_t batch_stride;
+    int64_t head_stride;
+    int64_t row_stride;
+} wrs_layout;
+
+/* ---- lifecycle ---------------------------------------------------------
+ * No reference counterpart: the reference computes on host threads. The
+ * context is what WhisperState would hold when whisper_context_params.use_gpu
+ * / gpu_device (include/whisper.h:126-129) select this backend. */
+int wrs_attn_create(int device, wrs_attn_ctx **out);
+void wrs_attn_destroy(wrs_attn_ctx *ctx);
+/* Queue work on a caller-owned hipStream_t; NULL is the device's null
+ * (default) stream. A new context starts on a stream of its own. */
+int wrs_attn_set_stream(wrs_attn_ctx *ctx, void *hip_stream);
+void *wrs_attn_get_stream(wrs_attn_ctx *ctx);
+int wrs_attn_synchronize(wrs_attn_ctx *ctx);
+/* Text of the last error on this context (valid until the next call). */
+const char *wrs_attn_last_error(wrs_attn_ctx *ctx);
+const char *wrs_attn_status_string(int status);
+
+/* ---- host-slice drop-ins (synchronous; f32 host buffers) ---------------
+ * Same arguments, argument meaning and results as the reference functions,
+ * with slice lengths passed explicitly so the reference's length assertions
+ * can be checked. */
+
+/* pub fn flash_attention_2(q,k,v, t_q, t_kv, n_heads, d_model, causal, output)
+ * crates/tensor/src/ops/attention.rs:68-78 (asserts :79-88). */
+int wrs_flash_attention_2(wrs_attn_ctx *ctx, const float *q, size_t q_len, const float *k,
+                          size_t k_len, const float *v, size_t v_len, size_t t_q, size_t t_kv,
+                          size_t n_heads, size_t d_model, int causal, float *output,
+                          size_t output_len);
+
+/* pub fn multi_head_attention(...) -- same signature,
+ * crates/tensor/src/ops/attention.rs:29-41. */
+int wrs_multi_head_attention(wrs_attn_ctx *ctx, const float *q, size_t q_len, const float *k,
+                             size_t k_len, const float *v, size_t v_len, size_t t_q, size_t t_kv,
+                             size_t n_heads, size_t d_model, int causal, float *output,
+                             size_t output_len);
+
+/* pub fn single_token_mha_d64(q,k,v, t_kv, n_heads, d_model, output)
+ * crates/tensor/src/ops/attention.rs:246-254. */
+int wrs_single_token_mha_d64(wrs_attn_ctx *ctx, const float *q, size_t q_len, const float *k,
+                             size_t k_len, const float *v, size_t v_len, size_t t_kv,
+                             size_t n_heads, size_t d_model, float *output, size_t output_len);
+
+/* fn multi_head_attention_with_cache(q,k,v, n_tokens, total_tokens, t_past,
+ * n_heads, d_model, output) -- crates/whisper/src/decoder.rs:835-892
+ * (private in the reference; exported so the decoder can route through it). */
+int wrs_mha_with_cache(wrs_attn_ctx *ctx, const float *q, size_t q_len, const float *k,
+                       size_t k_len, const float *v, size_t v_len, size_t n_tokens,
+                       size_t total_tokens, size_t t_past, size_t n_heads, size_t d_model,
+                       float *output, size_t output_len);
+
+/* ---- device-resident prefill (asynchronous) ----------------------------
+ * flash_attention_2 (crates/tensor/src/ops/attention.rs:68-243) over `batch`
+ * independent windows, called from crates/whisper/src/encoder.rs:289-299.
+ * q/k/v/out are device pointers; out is f32. Queries are causal-masked
+ * against keys j <= i + q_pos_offset when `causal` is set (q_pos_offset = 0
+ * is the reference's mask; t_past is the decoder prompt's,
+ * crates/whisper/src/decoder.rs:861). Supported types: q_dtype == kv_dtype
+ * in {F16, BF16} (d_head 64 runs on the 16-bit MFMA kernel, other d_head on
+ * the f32 one), and q F32 with kv F32/F16/BF16 (f32 accumulate-check kernel).
+ * d_head <= 128. 16-bit tensors need 16-byte aligned rows (strides multiple
+ * of 8 elements). */
+int wrs_attn_prefill(wrs_attn_ctx *ctx, int q_dtype, const void *q, const wrs_layout *q_layout,
+                     int kv_dtype, const void *k, const wrs_layout *k_layout, const void *v,
+                     const wrs_layout *v_layout, float *out, const wrs_layout *out_layout,
+                     size_t batch, size_t n_heads, size_t t_q, size_t t_kv, size_t d_head,
+                     int causal, size_t q_pos_offset);
+
+/* ---- device KV arena ---------------------------------------------------
+ * pub struct DecoderKvCache (crates/whisper/src/decoder.rs:131-145), in HBM:
+ * self K/V f16 [layer][slot][head][max_ctx][64], cross K/V f16
+ * [layer][head][n_audio_max][64]; d_head is 64, d_model = n_heads*64.
+ * Slot lengths (the reference's t_past vector) are kept on the host. */
+
+/* DecoderKvCache::new (decoder.rs:148-157) with the arena capacity fixed. */
+int wrs_kv_create(wrs_attn_ctx *ctx, size_t n_layers, size_t n_slots, size_t n_heads,
+                  size_t max_ctx, size_t n_audio_max, wrs_kv **out);
+void wrs_kv_destroy(wrs_kv *kv);
+/* DecoderKvCache::clear (decoder.rs:162-176): every slot length to 0. */
+int wrs_kv_clear(wrs_kv *kv);
+/* DecoderKvCache::clear_slot (decoder.rs:179-189). */
+int wrs_kv_clear_slot(wrs_kv *kv, size_t slot);
+/* DecoderKvCache::invalidate_cross (decoder.rs:196-203). */
+int wrs_kv_invalidate_cross(wrs_kv *kv);
+/* DecoderKvCache::ensure_slots (decoder.rs:207-218): grows, keeps contents. */
+int wrs_kv_ensure_slots(wrs_kv *kv, size_t n_slots);
+/* DecoderKvCache::copy_slot (decoder.rs:223-236): valid prefix of src -> dst. */
+int wrs_kv_copy_slot(wrs_kv *kv, size_t dst, size_t src);
+/* DecoderKvCache::slot_len (decoder.rs:239-241). */
+int wrs_kv_slot_len(wrs_kv *kv, size_t slot, size_t *len);
+/* `cache.t_past[slot] = n_past` rewind (crates/ffi/src/lib.rs:2352 with the
+ * truncation at decoder.rs:626-630); len must not exceed the stored rows. */
+int wrs_kv_set_len(wrs_kv *kv, size_t slot, size_t len);
+/* DecoderKvCache::slide_to_fit (decoder.rs:248-263); *pos gets t_past. */
+int wrs_kv_slide_to_fit(wrs_kv *kv, size_t slot, size_t n_new, size_t max_ctx, size_t *pos);
+/* Append of decoder.rs:631-635: write n rows (f32 [n][d_model]) of this
+ * layer's K and V at the slot's current length; lengths advance only with
+ * wrs_kv_advance, after all layers (decoder.rs:765-767). src_on_host selects
+ * host or device source pointers. */
+int wrs_kv_append(wrs_kv *kv, size_t layer, size_t slot, const float *k_rows,
+                  const float *v_rows, size_t n, int src_on_host);
+int wrs_kv_advance(wrs_kv *kv, size_t slot, size_t n);
+/* Store of precompute_cross_attn (decoder.rs:423-447): f32 [n_audio][d_model]
+ * K and V of one layer, converted to f16 head planes. */
+int wrs_kv_set_cross(wrs_kv *kv, size_t layer, const float *k, const float *v, size_t n_audio,
+                     int src_on_host);
+int wrs_kv_cross_len(wrs_kv *kv, size_t *n_audio);
+/* Raw device pointers of the arena planes (for tests and fused callers). */
+int wrs_kv_self_planes(wrs_kv *kv, void **k, void **v, size_t *slot_stride_elems);
+int wrs_kv_cross_planes(wrs_kv *kv, void **k, void **v);
+
+/* ---- device-resident decode (asynchronous) -----------------------------
+ * Self-attention step: decoder.rs:613-647 -> multi_head_attention_with_cache
+ * -> single_token_mha_d64 (decoder.rs:852-855) for every slot in one launch.
+ * Row i of q ([n][d_model] f32, device) belongs to slots[i] (host array) and
+ * sits at position slot_len(slots[i]); its K/V row must already be appended,
+ * so it attends slot_len + 1 keys. out: [n][d_model] f32 device. */
+int wrs_attn_decode_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const size_t *slots,
+                         size_t n, const float *q, float *out);
+/* Cross-attention step: decoder.rs:689-724 -> multi_head_attention ->
+ * single_token_mha_d64 (attention.rs:102-105), all n_beams query rows of one
+ * utterance against the shared cross plane in one launch (K/V read once). */
+int wrs_attn_decode_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
+                          size_t n_beams, float *out);
+/* Multi-token rows (prompt prefill): decoder.rs:857-891 self-attention with
+ * offset t_past = slot_len(slot) over the slot's f16 cache (rows appended),
+ * and attention.rs:107-243 cross-attention with t_q = n_tokens. */
+int wrs_attn_prefill_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, size_t slot,
+                          const float *q, size_t n_tokens, float *out);
+int wrs_attn_prefill_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
+                           size_t n_tokens, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WRS_ATTN_H */

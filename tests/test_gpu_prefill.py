@@ -1,0 +1,246 @@
+"""GPU parity of the prefill path (encoder self-attention, prompt rows) against
+the CPU oracle, through the C ABI.
+
+Bars: 1e-5 max-abs for f32 inputs (the reference's own tiled-vs-materialized
+bound, crates/tensor/tests/test_flash_attention_tiled.rs:126), 2e-3 for
+f16/bf16 inputs (values widened exactly to f32 for the oracle).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import dev, host, maxerr, note
+from refmath import attention_f64
+from test_oracle import KAT_SHAPES, _kat_inputs, _modular_inputs
+
+pytestmark = pytest.mark.gpu
+
+TOL16 = 2e-3
+TOL32 = 1e-5
+
+
+@pytest.fixture(scope="module")
+def ctx(wrs):
+    c = wrs.Context(0)
+    c.use_torch_stream()
+    return c
+
+
+def _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal=False):
+    out = np.zeros(t_q * d_model, np.float32)
+    orc.flash_attention_2(np.ascontiguousarray(q.ravel()), np.ascontiguousarray(k.ravel()),
+                          np.ascontiguousarray(v.ravel()), t_q, t_kv, n_heads, d_model, causal,
+                          out)
+    return out.reshape(t_q, d_model)
+
+
+# ---- host-slice drop-in: the reference's own known-answer tests -----------
+
+@pytest.mark.parametrize("t_q,t_kv,h,dh,causal", KAT_SHAPES)
+def test_host_slice_kat(wrs, orc, ctx, t_q, t_kv, h, dh, causal):
+    note(f"host-slice flash_attention_2 t_q={t_q} t_kv={t_kv} h={h} dh={dh} causal={causal}")
+    d_model, q, k, v = _kat_inputs(orc, t_q, t_kv, h, dh)
+    out = np.full(t_q * d_model, np.nan, np.float32)
+    wrs.flash_attention_2(q, k, v, t_q, t_kv, h, d_model, causal, out, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, h, d_model, causal)
+    orc_out = _oracle_fa2(orc, q, k, v, t_q, t_kv, h, d_model, causal)
+    assert maxerr(out.reshape(t_q, d_model), orc_out) <= TOL32
+    assert maxerr(out.reshape(t_q, d_model), ref) <= TOL32
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_host_slice_modular_inputs(wrs, orc, ctx, causal):
+    # crates/tensor/tests/test_flash_attention.rs:3-98 (d_head 16, bound 1e-4)
+    t_q, t_kv, n_heads, d_model = 64, 128, 4, 64
+    note(f"host-slice modular inputs causal={causal}")
+    q, k, v = _modular_inputs(t_q, t_kv, d_model)
+    out = np.zeros(t_q * d_model, np.float32)
+    wrs.multi_head_attention(q, k, v, t_q, t_kv, n_heads, d_model, causal, out, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, n_heads, d_model, causal)
+    assert maxerr(out.reshape(t_q, d_model), ref) <= 1e-4
+    assert maxerr(out.reshape(t_q, d_model),
+                  _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal)) <= TOL32
+
+
+def test_host_slice_causal_single_query_sees_first_key(wrs, orc, ctx):
+    # test_flash_attention_tiled.rs:186-205
+    note("host-slice causal single query")
+    d_model, t_kv = 64, 17
+    rng = orc.Rng(0xFEED_FACE)
+    q, k, v = rng.fill(d_model), rng.fill(t_kv * d_model), rng.fill(t_kv * d_model)
+    out = np.zeros(d_model, np.float32)
+    wrs.flash_attention_2(q, k, v, 1, t_kv, 1, d_model, True, out, ctx=ctx)
+    assert np.all(np.abs(out - v[:d_model]) <= 1e-6)
+
+
+def test_host_slice_overwrites_stale_output(wrs, orc, ctx):
+    # test_flash_attention_tiled.rs:243-262
+    note("host-slice stale NaN sentinel")
+    t_q, t_kv, n_heads, d_model = 40, 100, 2, 128
+    rng = orc.Rng(0xDEAD_BEEF)
+    q, k, v = rng.fill(t_q * d_model), rng.fill(t_kv * d_model), rng.fill(t_kv * d_model)
+    out = np.full(t_q * d_model, np.nan, np.float32)
+    wrs.flash_attention_2(q, k, v, t_q, t_kv, n_heads, d_model, True, out, ctx=ctx)
+    assert np.all(np.isfinite(out))
+
+
+def test_host_slice_edges_and_asserts(wrs, ctx):
+    note("host-slice edge cases")
+    d_model = 128
+    k = np.ones(5 * d_model, np.float32)
+    # t_q == 0: no-op (attention.rs:90-92)
+    wrs.flash_attention_2(np.zeros(0, np.float32), k, k, 0, 5, 2, d_model, False,
+                          np.zeros(0, np.float32), ctx=ctx)
+    # t_kv == 0: zero fill (attention.rs:93-96)
+    out = np.full(3 * d_model, np.nan, np.float32)
+    e = np.zeros(0, np.float32)
+    wrs.flash_attention_2(np.ones(3 * d_model, np.float32), e, e, 3, 0, 2, d_model, False, out,
+                          ctx=ctx)
+    assert np.all(out == 0.0)
+    q = np.zeros(d_model, np.float32)
+    with pytest.raises(AssertionError):  # n_heads == 0 (attention.rs:79)
+        wrs.flash_attention_2(q, q, q, 1, 1, 0, d_model, False, q.copy(), ctx=ctx)
+    with pytest.raises(AssertionError):  # d_model % n_heads (:80-83)
+        wrs.flash_attention_2(q, q, q, 1, 1, 3, d_model, False, q.copy(), ctx=ctx)
+    with pytest.raises(AssertionError):  # q.len() != t_q*d_model (:85)
+        wrs.flash_attention_2(q, q, q, 2, 1, 2, d_model, False, q.copy(), ctx=ctx)
+
+
+# ---- device-resident prefill on the BASELINE-shaped workloads -------------
+
+def _encoder_run(wrs, ctx, cfg, q, k, v, dtype, batch=None):
+    b = q.shape[0] if batch is None else batch
+    T, dm = cfg.t, cfg.d_model
+    qd, kd, vd = dev(q, dtype), dev(k, dtype), dev(v, dtype)
+    out = torch.full((b, T, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lay = wrs.token_major(T, dm, 64)
+    wrs.prefill(qd, kd, vd, out, batch=b, n_heads=cfg.n_heads, t_q=T, t_kv=T, d_head=64,
+                q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+    return host(out)
+
+
+def test_tiny_encoder_f32(wrs, orc, ctx):
+    from wrs_amd import workloads as W
+    cfg = W.TINY_ENCODER
+    note(f"device prefill f32: {cfg.name}")
+    q, k, v = cfg.inputs()
+    out = _encoder_run(wrs, ctx, cfg, q, k, v, torch.float32)
+    ref = _oracle_fa2(orc, q[0], k[0], v[0], cfg.t, cfg.t, cfg.n_heads, cfg.d_model)
+    assert maxerr(out[0], ref) <= TOL32
+
+
+def test_base_encoder_f16(wrs, orc, ctx):
+    from wrs_amd import workloads as W
+    cfg = W.BASE_ENCODER
+    note(f"device prefill f16 MFMA: {cfg.name}")
+    q, k, v = cfg.inputs()
+    out = _encoder_run(wrs, ctx, cfg, q, k, v, torch.float16)
+    for w in range(cfg.batch):
+        ref = _oracle_fa2(orc, q[w], k[w], v[w], cfg.t, cfg.t, cfg.n_heads, cfg.d_model)
+        assert maxerr(out[w], ref) <= TOL16, f"window {w}"
+
+
+def test_large_encoder_bf16(wrs, orc, ctx):
+    from wrs_amd import workloads as W
+    cfg = W.LARGE_ENCODER
+    note(f"device prefill bf16 MFMA: {cfg.name}")
+    q, k, v = cfg.inputs()
+    out = _encoder_run(wrs, ctx, cfg, q, k, v, torch.bfloat16)
+    assert np.all(np.isfinite(out))
+    # oracle on the first and last window, all 20 heads
+    for w in (0, cfg.batch - 1):
+        ref = _oracle_fa2(orc, q[w], k[w], v[w], cfg.t, cfg.t, cfg.n_heads, cfg.d_model)
+        assert maxerr(out[w], ref) <= TOL16, f"window {w}"
+    # every window: each output is a convex combination of that head's V rows
+    vmin = v.min(axis=1)
+    vmax = v.max(axis=1)
+    assert np.all(out >= vmin[:, None, :] - 1e-3) and np.all(out <= vmax[:, None, :] + 1e-3)
+    # a window computed alone equals the same window inside the batch, bitwise
+    note("device prefill bf16: window 7 alone")
+    alone = _encoder_run(wrs, ctx, cfg, q[7:8], k[7:8], v[7:8], torch.bfloat16, batch=1)
+    assert np.array_equal(alone[0], out[7])
+
+
+def test_fused_qkv_row_layout(wrs, ctx):
+    # q/k/v as column slices of one [B][T][3*d_model] projection output
+    # (crates/whisper/src/encoder.rs:275-287) give the same bits as packed rows.
+    from wrs_amd import workloads as W
+    B, H, T = 2, 8, 300
+    dm = H * 64
+    note("device prefill f16: fused QKV row layout")
+    x = W.normal((B, T, 3 * dm), 7, storage="f16")
+    xd = dev(x, torch.float16)
+    out_a = torch.empty((B, T, dm), dtype=torch.float32, device="cuda")
+    la = wrs.token_major(T, dm, 64, row_stride=3 * dm)
+    lo = wrs.token_major(T, dm, 64)
+    wrs.prefill(xd[..., :dm], xd[..., dm:2 * dm], xd[..., 2 * dm:], out_a, batch=B, n_heads=H,
+                t_q=T, t_kv=T, d_head=64, q_layout=la, kv_layout=la, out_layout=lo, ctx=ctx)
+    qd = xd[..., :dm].contiguous()
+    kd = xd[..., dm:2 * dm].contiguous()
+    vd = xd[..., 2 * dm:].contiguous()
+    out_b = torch.empty_like(out_a)
+    wrs.prefill(qd, kd, vd, out_b, batch=B, n_heads=H, t_q=T, t_kv=T, d_head=64, q_layout=lo,
+                kv_layout=lo, out_layout=lo, ctx=ctx)
+    assert torch.equal(out_a, out_b)
+
+
+RAGGED = [(1, 1), (1, 1500), (37, 63), (128, 64), (129, 65), (300, 257), (64, 1500),
+          (1500, 100)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("t_q,t_kv", RAGGED)
+def test_prefill_ragged_shapes(wrs, orc, ctx, dtype, t_q, t_kv):
+    from wrs_amd import workloads as W
+    H = 3
+    dm = H * 64
+    note(f"device prefill {dtype} ragged t_q={t_q} t_kv={t_kv}")
+    q = W.normal((t_q, dm), 11, storage=dtype)
+    k = W.normal((t_kv, dm), 12, storage=dtype)
+    v = W.normal((t_kv, dm), 13, storage=dtype)
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    out = torch.full((t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+    wrs.prefill(dev(q, tdt), dev(k, tdt), dev(v, tdt), out, batch=1, n_heads=H, t_q=t_q,
+                t_kv=t_kv, d_head=64, q_layout=lq, kv_layout=lk, out_layout=lq, ctx=ctx)
+    ref = _oracle_fa2(orc, q, k, v, t_q, t_kv, H, dm)
+    assert maxerr(host(out), ref) <= TOL16
+
+
+@pytest.mark.parametrize("t_q,t_kv,offset", [(5, 12, 7), (100, 137, 37), (128, 448, 320),
+                                             (90, 33, 0), (168, 37, 0)])
+def test_prefill_causal_with_offset(wrs, ctx, t_q, t_kv, offset):
+    from wrs_amd import workloads as W
+    H = 2
+    dm = H * 64
+    note(f"device prefill f16 causal t_q={t_q} t_kv={t_kv} offset={offset}")
+    q = W.normal((t_q, dm), 21, storage="f16")
+    k = W.normal((t_kv, dm), 22, storage="f16")
+    v = W.normal((t_kv, dm), 23, storage="f16")
+    out = torch.full((t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+    wrs.prefill(dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16), out,
+                batch=1, n_heads=H, t_q=t_q, t_kv=t_kv, d_head=64, q_layout=lq, kv_layout=lk,
+                out_layout=lq, causal=True, q_pos_offset=offset, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, H, dm, causal=True, q_offset=offset)
+    assert maxerr(host(out), ref) <= TOL16
+
+
+def test_prefill_d_head_80_f16_inputs(wrs, ctx):
+    # d_head != 64 with 16-bit inputs runs the f32-MFMA kernel on widened values.
+    from wrs_amd import workloads as W
+    H, dh, t_q, t_kv = 2, 80, 37, 91
+    dm = H * dh
+    note("device prefill f16 d_head=80")
+    q = W.normal((t_q, dm), 31, storage="f16")
+    k = W.normal((t_kv, dm), 32, storage="f16")
+    v = W.normal((t_kv, dm), 33, storage="f16")
+    out = torch.zeros((t_q, dm), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, dh), wrs.token_major(t_kv, dm, dh)
+    wrs.prefill(dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16), out,
+                batch=1, n_heads=H, t_q=t_q, t_kv=t_kv, d_head=dh, q_layout=lq, kv_layout=lk,
+                out_layout=lq, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, H, dm)
+    assert maxerr(host(out), ref) <= TOL32

@@ -1,0 +1,304 @@
+"""whisper.rs attention path on AMD Instinct MI355X (gfx950).
+
+Host-side mirror of the reference's attention interface over the C ABI of
+``include/wrs_attn.h`` (library ``lib/libwrs_attn.so``):
+
+* reference-named host-slice functions with the reference's argument meaning
+  and error behaviour -- ``flash_attention_2`` / ``multi_head_attention``
+  (crates/tensor/src/ops/attention.rs:29-243), ``single_token_mha_d64``
+  (attention.rs:246-434) and ``mha_with_cache``
+  (crates/whisper/src/decoder.rs:835-892). They take float32 numpy arrays;
+  a shape violation that panics in the reference raises ``AssertionError``.
+* device-resident entry points on torch tensors (torch supplies device memory
+  and the stream; every FLOP runs in this package's HIP kernels):
+  ``prefill`` and the ``KvArena`` (DecoderKvCache, decoder.rs:131-264) with
+  its ``decode_self`` / ``decode_cross`` / ``prefill_self`` / ``prefill_cross``.
+
+There is no CPU fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import numpy as np
+
+from . import _lib as _L
+from ._lib import (WRS_BF16, WRS_EINVAL, WRS_F16, WRS_F32, WRS_OK, ExtensionMissing, Layout,
+                   header_symbols)
+
+Q_TILE = 128  # crates/tensor/src/ops/attention.rs:13 (reference tile constants)
+KV_TILE = 128  # crates/tensor/src/ops/attention.rs:26
+
+__all__ = [
+    "Context", "KvArena", "ExtensionMissing", "Layout", "flash_attention_2",
+    "multi_head_attention", "single_token_mha_d64", "mha_with_cache", "prefill",
+    "token_major", "default_context", "header_symbols", "Q_TILE", "KV_TILE",
+]
+
+
+class Context:
+    """One device, one stream, private scratch (``wrs_attn_ctx``)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = _L.lib()
+        h = ctypes.c_void_p()
+        rc = self._lib.wrs_attn_create(int(device), ctypes.byref(h))
+        if rc != WRS_OK:
+            raise RuntimeError(f"wrs_attn_create(device={device}) failed: "
+                               f"{_L.status_string(rc)}")
+        self.handle = h
+        self.device = int(device)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self._lib.wrs_attn_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc: int, what: str) -> None:
+        if rc == WRS_OK:
+            return
+        msg = self._lib.wrs_attn_last_error(self.handle).decode()
+        if rc == WRS_EINVAL:
+            # The reference panics on these (assert!/assert_eq!).
+            raise AssertionError(f"{what}: {msg}")
+        raise RuntimeError(f"{what}: {_L.status_string(rc)}: {msg}")
+
+    def set_stream(self, stream_handle: int | None) -> None:
+        """Queue work on a hipStream_t handle; 0/None is the null stream."""
+        self.check(self._lib.wrs_attn_set_stream(self.handle, stream_handle or None),
+                   "wrs_attn_set_stream")
+
+    def use_torch_stream(self) -> None:
+        """Queue work on torch's current stream of this device."""
+        import torch
+        self.set_stream(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def synchronize(self) -> None:
+        self.check(self._lib.wrs_attn_synchronize(self.handle), "wrs_attn_synchronize")
+
+
+_default = None
+_default_lock = threading.Lock()
+
+
+def default_context() -> Context:
+    global _default
+    with _default_lock:
+        if _default is None:
+            _default = Context(0)
+        return _default
+
+
+# --------------------------------------------------------------------------
+# host-slice drop-ins (reference signatures)
+# --------------------------------------------------------------------------
+
+def _f32(a, name):
+    if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]):
+        raise TypeError(f"{name} must be a C-contiguous float32 numpy array")
+    return a.ctypes.data_as(ctypes.c_void_p), a.size
+
+
+def flash_attention_2(q, k, v, t_q, t_kv, n_heads, d_model, causal, output, ctx=None):
+    """crates/tensor/src/ops/attention.rs:68-78 on the GPU (synchronous)."""
+    ctx = ctx or default_context()
+    (pq, nq), (pk, nk), (pv, nv), (po, no) = (_f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
+                                              _f32(output, "output"))
+    ctx.check(ctx._lib.wrs_flash_attention_2(ctx.handle, pq, nq, pk, nk, pv, nv, t_q, t_kv,
+                                             n_heads, d_model, int(bool(causal)), po, no),
+              "flash_attention_2")
+
+
+def multi_head_attention(q, k, v, t_q, t_kv, n_heads, d_model, causal, output, ctx=None):
+    """crates/tensor/src/ops/attention.rs:29-41 on the GPU (synchronous)."""
+    ctx = ctx or default_context()
+    (pq, nq), (pk, nk), (pv, nv), (po, no) = (_f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
+                                              _f32(output, "output"))
+    ctx.check(ctx._lib.wrs_multi_head_attention(ctx.handle, pq, nq, pk, nk, pv, nv, t_q, t_kv,
+                                                n_heads, d_model, int(bool(causal)), po, no),
+              "multi_head_attention")
+
+
+def single_token_mha_d64(q, k, v, t_kv, n_heads, d_model, output, ctx=None):
+    """crates/tensor/src/ops/attention.rs:246-254 on the GPU (synchronous)."""
+    ctx = ctx or default_context()
+    (pq, nq), (pk, nk), (pv, nv), (po, no) = (_f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
+                                              _f32(output, "output"))
+    ctx.check(ctx._lib.wrs_single_token_mha_d64(ctx.handle, pq, nq, pk, nk, pv, nv, t_kv,
+                                                n_heads, d_model, po, no),
+              "single_token_mha_d64")
+
+
+def mha_with_cache(q, k, v, n_tokens, total_tokens, t_past, n_heads, d_model, output, ctx=None):
+    """crates/whisper/src/decoder.rs:835-892 on the GPU (synchronous)."""
+    ctx = ctx or default_context()
+    (pq, nq), (pk, nk), (pv, nv), (po, no) = (_f32(q, "q"), _f32(k, "k"), _f32(v, "v"),
+                                              _f32(output, "output"))
+    ctx.check(ctx._lib.wrs_mha_with_cache(ctx.handle, pq, nq, pk, nk, pv, nv, n_tokens,
+                                          total_tokens, t_past, n_heads, d_model, po, no),
+              "multi_head_attention_with_cache")
+
+
+# --------------------------------------------------------------------------
+# device-resident entry points (torch tensors as device memory)
+# --------------------------------------------------------------------------
+
+_DT = {"torch.float32": WRS_F32, "torch.float16": WRS_F16, "torch.bfloat16": WRS_BF16}
+
+
+def _dtype_code(t):
+    try:
+        return _DT[str(t.dtype)]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def token_major(t_rows: int, d_model: int, d_head: int, row_stride: int | None = None) -> Layout:
+    """Layout of the reference's [T][d_model] rows (optionally inside wider rows)."""
+    rs = d_model if row_stride is None else row_stride
+    return Layout(t_rows * rs, d_head, rs)
+
+
+def prefill(q, k, v, out, *, batch, n_heads, t_q, t_kv, d_head, q_layout, kv_layout, out_layout,
+            causal=False, q_pos_offset=0, k_layout=None, ctx=None):
+    """Batched flash_attention_2 over device tensors (asynchronous on ctx's stream)."""
+    ctx = ctx or default_context()
+    if out.dtype.__str__() != "torch.float32":
+        raise TypeError("out must be float32")
+    kl = k_layout or kv_layout
+    ctx.check(ctx._lib.wrs_attn_prefill(
+        ctx.handle, _dtype_code(q), q.data_ptr(), ctypes.byref(q_layout), _dtype_code(k),
+        k.data_ptr(), ctypes.byref(kl), v.data_ptr(), ctypes.byref(kv_layout), out.data_ptr(),
+        ctypes.byref(out_layout), batch, n_heads, t_q, t_kv, d_head, int(bool(causal)),
+        q_pos_offset), "wrs_attn_prefill")
+
+
+class KvArena:
+    """Device KV cache (``wrs_kv``), methods named after DecoderKvCache."""
+
+    def __init__(self, n_layers, n_slots, n_heads, max_ctx, n_audio_max, ctx=None):
+        self.ctx = ctx or default_context()
+        self._lib = self.ctx._lib
+        h = ctypes.c_void_p()
+        self.ctx.check(self._lib.wrs_kv_create(self.ctx.handle, n_layers, n_slots, n_heads,
+                                               max_ctx, n_audio_max, ctypes.byref(h)),
+                       "wrs_kv_create")
+        self.handle = h
+        self.n_layers, self.n_slots, self.n_heads = n_layers, n_slots, n_heads
+        self.max_ctx, self.n_audio_max = max_ctx, n_audio_max
+        self.d_model = n_heads * 64
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self._lib.wrs_kv_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _c(self, rc, what):
+        self.ctx.check(rc, what)
+
+    # DecoderKvCache methods (decoder.rs:162-263)
+    def clear(self):
+        self._c(self._lib.wrs_kv_clear(self.handle), "clear")
+
+    def clear_slot(self, slot):
+        self._c(self._lib.wrs_kv_clear_slot(self.handle, slot), "clear_slot")
+
+    def invalidate_cross(self):
+        self._c(self._lib.wrs_kv_invalidate_cross(self.handle), "invalidate_cross")
+
+    def ensure_slots(self, n_slots):
+        self._c(self._lib.wrs_kv_ensure_slots(self.handle, n_slots), "ensure_slots")
+        self.n_slots = max(self.n_slots, n_slots)
+
+    def copy_slot(self, dst, src):
+        self._c(self._lib.wrs_kv_copy_slot(self.handle, dst, src), "copy_slot")
+
+    def slot_len(self, slot) -> int:
+        n = ctypes.c_size_t()
+        self._c(self._lib.wrs_kv_slot_len(self.handle, slot, ctypes.byref(n)), "slot_len")
+        return n.value
+
+    def set_len(self, slot, n):
+        self._c(self._lib.wrs_kv_set_len(self.handle, slot, n), "set_len")
+
+    def slide_to_fit(self, slot, n_new, max_ctx) -> int:
+        pos = ctypes.c_size_t()
+        self._c(self._lib.wrs_kv_slide_to_fit(self.handle, slot, n_new, max_ctx,
+                                              ctypes.byref(pos)), "slide_to_fit")
+        return pos.value
+
+    @staticmethod
+    def _src(t):
+        if isinstance(t, np.ndarray):
+            p, n = _f32(t, "rows")
+            return p, n, 1
+        if str(t.dtype) != "torch.float32" or not t.is_contiguous():
+            raise TypeError("rows must be contiguous float32")
+        return t.data_ptr(), t.numel(), 0
+
+    def append(self, layer, slot, k_rows, v_rows):
+        pk, nk, host = self._src(k_rows)
+        pv, nv, host2 = self._src(v_rows)
+        assert nk == nv and nk % self.d_model == 0 and host == host2
+        self._c(self._lib.wrs_kv_append(self.handle, layer, slot, pk, pv, nk // self.d_model,
+                                        host), "append")
+
+    def advance(self, slot, n):
+        self._c(self._lib.wrs_kv_advance(self.handle, slot, n), "advance")
+
+    def set_cross(self, layer, k, v):
+        pk, nk, host = self._src(k)
+        pv, nv, host2 = self._src(v)
+        assert nk == nv and nk % self.d_model == 0 and host == host2
+        self._c(self._lib.wrs_kv_set_cross(self.handle, layer, pk, pv, nk // self.d_model, host),
+                "set_cross")
+
+    def cross_len(self) -> int:
+        n = ctypes.c_size_t()
+        self._c(self._lib.wrs_kv_cross_len(self.handle, ctypes.byref(n)), "cross_len")
+        return n.value
+
+    def plane_pointers(self):
+        ks, vs, kc, vc = (ctypes.c_void_p() for _ in range(4))
+        stride = ctypes.c_size_t()
+        self._c(self._lib.wrs_kv_self_planes(self.handle, ctypes.byref(ks), ctypes.byref(vs),
+                                             ctypes.byref(stride)), "self_planes")
+        self._c(self._lib.wrs_kv_cross_planes(self.handle, ctypes.byref(kc), ctypes.byref(vc)),
+                "cross_planes")
+        return ks.value, vs.value, kc.value, vc.value
+
+    # attention over the arena
+    def decode_self(self, layer, slots, q, out):
+        arr = (ctypes.c_size_t * len(slots))(*slots)
+        self._c(self._lib.wrs_attn_decode_self(self.ctx.handle, self.handle, layer, arr,
+                                               len(slots), q.data_ptr(), out.data_ptr()),
+                "decode_self")
+
+    def decode_cross(self, layer, q, out, n_beams=None):
+        n = q.shape[0] if n_beams is None else n_beams
+        self._c(self._lib.wrs_attn_decode_cross(self.ctx.handle, self.handle, layer,
+                                                q.data_ptr(), n, out.data_ptr()),
+                "decode_cross")
+
+    def prefill_self(self, layer, slot, q, out):
+        self._c(self._lib.wrs_attn_prefill_self(self.ctx.handle, self.handle, layer, slot,
+                                                q.data_ptr(), q.shape[0], out.data_ptr()),
+                "prefill_self")
+
+    def prefill_cross(self, layer, q, out):
+        self._c(self._lib.wrs_attn_prefill_cross(self.ctx.handle, self.handle, layer,
+                                                 q.data_ptr(), q.shape[0], out.data_ptr()),
+                "prefill_cross")

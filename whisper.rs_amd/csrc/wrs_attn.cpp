@@ -1,0 +1,816 @@
+// C-ABI runtime of the MI355X attention path: contexts (device + stream +
+// scratch), host-slice drop-ins, device-resident prefill/decode dispatch and
+// the device KV arena. Declarations and reference citations: include/wrs_attn.h.
+#include "../../include/wrs_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "wrs_internal.hpp"
+
+using wrs::DType;
+
+struct wrs_attn_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::string err;
+  // Device scratch, grown on demand and kept for the context's lifetime.
+  void* stage = nullptr;  // host-slice staging of q/k/v/out and score rows
+  size_t stage_bytes = 0;
+  float* part = nullptr;  // decode split partials
+  size_t part_bytes = 0;
+  unsigned* counters = nullptr;  // decode merge counters (kept zero between launches)
+  size_t counter_bytes = 0;
+};
+
+struct wrs_kv {
+  wrs_attn_ctx* ctx = nullptr;
+  size_t n_layers = 0, n_slots = 0, n_heads = 0, max_ctx = 0, n_audio_max = 0;
+  uint16_t* k_self = nullptr;  // f16 [layer][slot][head][max_ctx][64]
+  uint16_t* v_self = nullptr;
+  uint16_t* k_cross = nullptr;  // f16 [layer][head][n_audio_max][64]
+  uint16_t* v_cross = nullptr;
+  std::vector<size_t> len;        // per slot: rows stored (reference t_past)
+  std::vector<size_t> cross_len;  // per layer: n_audio of the stored cross K/V
+
+  size_t d_model() const { return n_heads * 64; }
+  size_t plane() const { return max_ctx * 64; }
+  size_t self_off(size_t layer, size_t slot) const {
+    return ((layer * n_slots + slot) * n_heads) * plane();
+  }
+  size_t cross_off(size_t layer) const { return layer * n_heads * n_audio_max * 64; }
+};
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+int fail(wrs_attn_ctx* c, int code, const char* what, hipError_t e = hipSuccess) {
+  if (c) {
+    c->err = what;
+    if (e != hipSuccess) {
+      c->err += ": ";
+      c->err += hipGetErrorString(e);
+    }
+  }
+  return code;
+}
+
+#define WRS_HIP(c, expr)                                        \
+  do {                                                          \
+    hipError_t e_ = (expr);                                     \
+    if (e_ != hipSuccess) return fail((c), WRS_EHIP, #expr, e_); \
+  } while (0)
+
+int grow(wrs_attn_ctx* c, void** p, size_t* cap, size_t bytes, bool zero) {
+  if (*cap >= bytes) return WRS_OK;
+  size_t want = std::max(bytes, *cap * 2);
+  if (*p) {
+    // The buffer may still be read by work queued on the stream.
+    WRS_HIP(c, hipStreamSynchronize(c->stream));
+    WRS_HIP(c, hipFree(*p));
+    *p = nullptr;
+    *cap = 0;
+  }
+  if (hipMalloc(p, want) != hipSuccess) {
+    *p = nullptr;
+    return fail(c, WRS_ENOMEM, "hipMalloc of context scratch failed");
+  }
+  *cap = want;
+  if (zero) WRS_HIP(c, hipMemsetAsync(*p, 0, want, c->stream));
+  return WRS_OK;
+}
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool fits_int(size_t x) { return x <= 0x7fffffffu; }
+
+// Host-slice staging area: carve f32 regions out of the context buffer.
+struct Stage {
+  std::vector<size_t> offs;
+  size_t total = 0;
+  size_t add(size_t floats) {
+    offs.push_back(total);
+    total += align_up(floats * sizeof(float), 256);
+    return offs.size() - 1;
+  }
+};
+
+float* stage_ptr(wrs_attn_ctx* c, const Stage& s, size_t i) {
+  return reinterpret_cast<float*>(static_cast<char*>(c->stage) + s.offs[i]);
+}
+
+int run_exact(wrs_attn_ctx* c, const float* q, size_t q_floats, const float* k, const float* v,
+              size_t kv_floats, float* out, size_t out_floats, int n_rows, int n_heads,
+              int d_head, int64_t d_model, int row_limit0) {
+  // Device copy of the inputs, exact-semantics kernel, copy back.
+  const size_t max_keys = static_cast<size_t>(row_limit0) + n_rows - 1;
+  Stage st;
+  const size_t iq = st.add(q_floats), ik = st.add(kv_floats), iv = st.add(kv_floats);
+  const size_t io = st.add(out_floats);
+  const size_t is = st.add(static_cast<size_t>(n_rows) * n_heads * std::max<size_t>(max_keys, 1));
+  int rc = grow(c, &c->stage, &c->stage_bytes, st.total, false);
+  if (rc) return rc;
+  float *dq = stage_ptr(c, st, iq), *dk = stage_ptr(c, st, ik), *dv = stage_ptr(c, st, iv);
+  float *dout = stage_ptr(c, st, io), *ds = stage_ptr(c, st, is);
+  WRS_HIP(c, hipMemcpyAsync(dq, q, q_floats * 4, hipMemcpyHostToDevice, c->stream));
+  if (kv_floats) {
+    WRS_HIP(c, hipMemcpyAsync(dk, k, kv_floats * 4, hipMemcpyHostToDevice, c->stream));
+    WRS_HIP(c, hipMemcpyAsync(dv, v, kv_floats * 4, hipMemcpyHostToDevice, c->stream));
+  }
+  wrs::ExactArgs a{};
+  a.q = dq;
+  a.k = dk;
+  a.v = dv;
+  a.o = dout;
+  a.q_rs = d_model;
+  a.kv_rs = d_model;
+  a.o_rs = d_model;
+  a.n_rows = n_rows;
+  a.n_heads = n_heads;
+  a.d_head = d_head;
+  a.row_limit0 = row_limit0;
+  a.scale = 1.0f / std::sqrt(static_cast<float>(d_head));
+  a.scores = ds;
+  a.scores_stride = static_cast<int64_t>(std::max<size_t>(max_keys, 1));
+  WRS_HIP(c, wrs::launch_decode_exact_f32(a, c->stream));
+  WRS_HIP(c, hipMemcpyAsync(out, dout, out_floats * 4, hipMemcpyDeviceToHost, c->stream));
+  WRS_HIP(c, hipStreamSynchronize(c->stream));
+  return WRS_OK;
+}
+
+int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& lq, int kv_dtype,
+                 const void* k, const wrs_layout& lk, const void* v, const wrs_layout& lv,
+                 float* out, const wrs_layout& lo, size_t batch, size_t n_heads, size_t t_q,
+                 size_t t_kv, size_t d_head, int causal, size_t q_pos_offset) {
+  if (batch == 0 || n_heads == 0 || t_q == 0) return WRS_OK;
+  if (!q || !out || (t_kv && (!k || !v))) return fail(c, WRS_EINVAL, "null tensor pointer");
+  if (d_head == 0 || d_head > 128) return fail(c, WRS_EUNSUPPORTED, "d_head must be 1..128");
+  if (!fits_int(batch) || !fits_int(n_heads) || !fits_int(t_q) || !fits_int(t_kv) ||
+      !fits_int(q_pos_offset) || !fits_int(t_q + q_pos_offset))
+    return fail(c, WRS_EINVAL, "dimension exceeds 2^31");
+  const bool same16 = q_dtype == kv_dtype && (q_dtype == WRS_F16 || q_dtype == WRS_BF16);
+  const bool q32 = q_dtype == WRS_F32 &&
+                   (kv_dtype == WRS_F32 || kv_dtype == WRS_F16 || kv_dtype == WRS_BF16);
+  if (!same16 && !q32) return fail(c, WRS_EUNSUPPORTED, "unsupported q/kv dtype combination");
+
+  wrs::PrefillArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = out;
+  a.lq = {lq.batch_stride, lq.head_stride, lq.row_stride};
+  a.lk = {lk.batch_stride, lk.head_stride, lk.row_stride};
+  a.lv = {lv.batch_stride, lv.head_stride, lv.row_stride};
+  a.lo = {lo.batch_stride, lo.head_stride, lo.row_stride};
+  a.batch = static_cast<int>(batch);
+  a.n_heads = static_cast<int>(n_heads);
+  a.t_q = static_cast<int>(t_q);
+  a.t_kv = static_cast<int>(t_kv);
+  a.d_head = static_cast<int>(d_head);
+  a.causal = causal ? 1 : 0;
+  a.q_pos_offset = static_cast<int>(q_pos_offset);
+  a.scale = 1.0f / std::sqrt(static_cast<float>(d_head));
+
+  if (t_kv == 0) {
+    // attention.rs:93-96: zero output. Rows of out may be strided.
+    for (size_t b = 0; b < batch; ++b)
+      for (size_t h = 0; h < n_heads; ++h)
+        WRS_HIP(c, hipMemset2DAsync(out + b * lo.batch_stride + h * lo.head_stride,
+                                    lo.row_stride * 4, 0, d_head * 4, t_q, c->stream));
+    return WRS_OK;
+  }
+
+  auto aligned16 = [](const void* p, const wrs_layout& l, int mult) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && l.batch_stride % mult == 0 &&
+           l.head_stride % mult == 0 && l.row_stride % mult == 0;
+  };
+  if (same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
+      aligned16(v, lv, 8) && aligned16(out, lo, 4)) {
+    WRS_HIP(c, wrs::launch_prefill_mfma16(a, q_dtype == WRS_F16 ? wrs::kF16 : wrs::kBF16,
+                                          c->stream));
+    return WRS_OK;
+  }
+  WRS_HIP(c, wrs::launch_prefill_f32(a, static_cast<DType>(q_dtype), static_cast<DType>(kv_dtype),
+                                     c->stream));
+  return WRS_OK;
+}
+
+int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64_t o_rs,
+                const uint16_t* kbase, const uint16_t* vbase, int64_t kv_hs,
+                const std::vector<int64_t>& goff, const std::vector<int>& lens, int rows_per_group,
+                int n_heads) {
+  const int n_groups = static_cast<int>(goff.size());
+  if (n_groups == 0) return WRS_OK;
+  if (n_groups > wrs::kMaxDecodeGroups || rows_per_group < 1 ||
+      rows_per_group > wrs::kMaxRowsPerGroup)
+    return fail(c, WRS_EINVAL, "decode batch shape");
+  wrs::DecodeArgs a{};
+  a.q = q;
+  a.o = out;
+  a.k = reinterpret_cast<const _Float16*>(kbase);
+  a.v = reinterpret_cast<const _Float16*>(vbase);
+  a.q_rs = q_rs;
+  a.o_rs = o_rs;
+  a.kv_hs = kv_hs;
+  int max_len = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    a.goff[g] = goff[g];
+    a.len[g] = lens[g];
+    max_len = std::max(max_len, lens[g]);
+  }
+  a.n_groups = n_groups;
+  a.rows_per_group = rows_per_group;
+  a.n_heads = n_heads;
+  a.chunk = 64;
+  a.n_splits = std::max(1, (max_len + 63) / 64);
+  a.scale_log2 = 0.125f * 1.4426950408889634f;
+  if (a.n_splits > 1) {
+    const size_t pb =
+        wrs::decode_part_floats(n_groups, n_heads, a.n_splits, rows_per_group) * sizeof(float);
+    int rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes, pb, false);
+    if (rc) return rc;
+    rc = grow(c, reinterpret_cast<void**>(&c->counters), &c->counter_bytes,
+              static_cast<size_t>(n_groups) * n_heads * sizeof(unsigned), true);
+    if (rc) return rc;
+  }
+  a.part = c->part;
+  a.counters = c->counters;
+  WRS_HIP(c, wrs::launch_decode_f16(a, c->stream));
+  return WRS_OK;
+}
+
+const float* to_device_f32(wrs_attn_ctx* c, const float* src, size_t floats, int on_host,
+                           size_t stage_offset_bytes, int* rc) {
+  *rc = WRS_OK;
+  if (!on_host) return src;
+  float* dst =
+      reinterpret_cast<float*>(static_cast<char*>(c->stage) + stage_offset_bytes);
+  hipError_t e = hipMemcpyAsync(dst, src, floats * 4, hipMemcpyHostToDevice, c->stream);
+  if (e != hipSuccess) *rc = fail(c, WRS_EHIP, "hipMemcpyAsync host->device", e);
+  return dst;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wrs_attn_status_string(int status) {
+  switch (status) {
+    case WRS_OK: return "ok";
+    case WRS_EINVAL: return "invalid argument (reference would panic)";
+    case WRS_ENOMEM: return "out of memory";
+    case WRS_EHIP: return "HIP runtime error";
+    case WRS_EUNSUPPORTED: return "unsupported on the GPU path";
+    case WRS_ERANGE: return "index or length outside the arena";
+    default: return "unknown status";
+  }
+}
+
+int wrs_attn_create(int device, wrs_attn_ctx** out) {
+  if (!out) return WRS_EINVAL;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return WRS_EINVAL;
+  auto* c = new (std::nothrow) wrs_attn_ctx();
+  if (!c) return WRS_ENOMEM;
+  c->device = device;
+  DeviceGuard g(device);
+  if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return WRS_EHIP;
+  }
+  c->stream = c->own_stream;
+  *out = c;
+  return WRS_OK;
+}
+
+void wrs_attn_destroy(wrs_attn_ctx* c) {
+  if (!c) return;
+  DeviceGuard g(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  if (c->stage) (void)hipFree(c->stage);
+  if (c->part) (void)hipFree(c->part);
+  if (c->counters) (void)hipFree(c->counters);
+  if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+int wrs_attn_set_stream(wrs_attn_ctx* c, void* s) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  c->stream = static_cast<hipStream_t>(s);
+  return WRS_OK;
+}
+
+void* wrs_attn_get_stream(wrs_attn_ctx* c) { return c ? c->stream : nullptr; }
+
+int wrs_attn_synchronize(wrs_attn_ctx* c) {
+  if (!c) return WRS_EINVAL;
+  DeviceGuard g(c->device);
+  WRS_HIP(c, hipStreamSynchronize(c->stream));
+  return WRS_OK;
+}
+
+const char* wrs_attn_last_error(wrs_attn_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int wrs_single_token_mha_d64(wrs_attn_ctx* c, const float* q, size_t q_len, const float* k,
+                             size_t k_len, const float* v, size_t v_len, size_t t_kv,
+                             size_t n_heads, size_t d_model, float* output, size_t output_len) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  // attention.rs:322-327 reads head h at h*64 of q/out and of every key row.
+  const size_t span = n_heads * 64;
+  if (span > d_model || q_len < span || output_len < span)
+    return fail(c, WRS_EINVAL, "single_token_mha_d64: head span exceeds q/output/d_model");
+  const size_t kv_need = t_kv ? (t_kv - 1) * d_model + span : 0;
+  if (k_len < kv_need || v_len < kv_need)
+    return fail(c, WRS_EINVAL, "single_token_mha_d64: k/v shorter than t_kv rows");
+  if (!fits_int(t_kv) || !fits_int(n_heads)) return fail(c, WRS_EINVAL, "dimension exceeds 2^31");
+  if (n_heads == 0) return WRS_OK;
+  if (t_kv == 0) {
+    std::memset(output, 0, span * sizeof(float));
+    return WRS_OK;
+  }
+  return run_exact(c, q, span, k, v, kv_need, output, span, 1, static_cast<int>(n_heads), 64,
+                   static_cast<int64_t>(d_model), static_cast<int>(t_kv));
+}
+
+int wrs_flash_attention_2(wrs_attn_ctx* c, const float* q, size_t q_len, const float* k,
+                          size_t k_len, const float* v, size_t v_len, size_t t_q, size_t t_kv,
+                          size_t n_heads, size_t d_model, int causal, float* output,
+                          size_t output_len) {
+  if (!c) return WRS_EINVAL;
+  // attention.rs:79-88
+  if (n_heads == 0) return fail(c, WRS_EINVAL, "n_heads must be non-zero");
+  if (d_model % n_heads != 0) return fail(c, WRS_EINVAL, "d_model is not divisible by n_heads");
+  if (q_len != t_q * d_model || k_len != t_kv * d_model || v_len != t_kv * d_model ||
+      output_len != t_q * d_model)
+    return fail(c, WRS_EINVAL, "flash_attention_2: slice length mismatch");
+  const size_t d_head = d_model / n_heads;
+  if (t_q == 0) return WRS_OK;  // :90-92
+  if (t_kv == 0) {              // :93-96
+    std::memset(output, 0, output_len * sizeof(float));
+    return WRS_OK;
+  }
+  if (t_q == 1 && d_head == 64 && !causal)  // :102-105
+    return wrs_single_token_mha_d64(c, q, q_len, k, k_len, v, v_len, t_kv, n_heads, d_model,
+                                    output, output_len);
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  if (d_head > 128) return fail(c, WRS_EUNSUPPORTED, "d_head > 128");
+  if (!fits_int(t_q) || !fits_int(t_kv) || !fits_int(n_heads))
+    return fail(c, WRS_EINVAL, "dimension exceeds 2^31");
+  Stage st;
+  const size_t iq = st.add(q_len), ik = st.add(k_len), iv = st.add(v_len), io = st.add(output_len);
+  int rc = grow(c, &c->stage, &c->stage_bytes, st.total, false);
+  if (rc) return rc;
+  float *dq = stage_ptr(c, st, iq), *dk = stage_ptr(c, st, ik), *dv = stage_ptr(c, st, iv);
+  float* dout = stage_ptr(c, st, io);
+  WRS_HIP(c, hipMemcpyAsync(dq, q, q_len * 4, hipMemcpyHostToDevice, c->stream));
+  WRS_HIP(c, hipMemcpyAsync(dk, k, k_len * 4, hipMemcpyHostToDevice, c->stream));
+  WRS_HIP(c, hipMemcpyAsync(dv, v, v_len * 4, hipMemcpyHostToDevice, c->stream));
+  const int64_t dm = static_cast<int64_t>(d_model), dh = static_cast<int64_t>(d_head);
+  const wrs_layout tq{0, dh, dm};
+  rc = prefill_impl(c, WRS_F32, dq, tq, WRS_F32, dk, tq, dv, tq, dout, tq, 1, n_heads, t_q, t_kv,
+                    d_head, causal, 0);
+  if (rc) return rc;
+  WRS_HIP(c, hipMemcpyAsync(output, dout, output_len * 4, hipMemcpyDeviceToHost, c->stream));
+  WRS_HIP(c, hipStreamSynchronize(c->stream));
+  return WRS_OK;
+}
+
+int wrs_multi_head_attention(wrs_attn_ctx* c, const float* q, size_t q_len, const float* k,
+                             size_t k_len, const float* v, size_t v_len, size_t t_q, size_t t_kv,
+                             size_t n_heads, size_t d_model, int causal, float* output,
+                             size_t output_len) {
+  // attention.rs:29-41 forwards unchanged.
+  return wrs_flash_attention_2(c, q, q_len, k, k_len, v, v_len, t_q, t_kv, n_heads, d_model,
+                               causal, output, output_len);
+}
+
+int wrs_mha_with_cache(wrs_attn_ctx* c, const float* q, size_t q_len, const float* k,
+                       size_t k_len, const float* v, size_t v_len, size_t n_tokens,
+                       size_t total_tokens, size_t t_past, size_t n_heads, size_t d_model,
+                       float* output, size_t output_len) {
+  if (!c) return WRS_EINVAL;
+  if (n_heads == 0 || d_model % n_heads != 0)
+    return fail(c, WRS_EINVAL, "mha_with_cache: n_heads must divide d_model");
+  // decoder.rs:846-850
+  if (q_len != n_tokens * d_model || k_len != total_tokens * d_model ||
+      v_len != total_tokens * d_model || output_len != n_tokens * d_model)
+    return fail(c, WRS_EINVAL, "mha_with_cache: slice length mismatch");
+  const size_t d_head = d_model / n_heads;
+  if (n_tokens == 0) return WRS_OK;
+  // Query i reads scores[0..=t_past+i] of a total_tokens buffer (decoder.rs:862-866).
+  if (t_past + n_tokens > total_tokens)
+    return fail(c, WRS_EINVAL, "mha_with_cache: t_past + n_tokens exceeds total_tokens");
+  if (n_tokens == 1 && d_head == 64)  // decoder.rs:852-855
+    return wrs_single_token_mha_d64(c, q, q_len, k, k_len, v, v_len, t_past + 1, n_heads,
+                                    d_model, output, output_len);
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  if (d_head > 128) return fail(c, WRS_EUNSUPPORTED, "d_head > 128");
+  if (!fits_int(total_tokens) || !fits_int(n_tokens) || !fits_int(n_heads))
+    return fail(c, WRS_EINVAL, "dimension exceeds 2^31");
+  return run_exact(c, q, q_len, k, v, (t_past + n_tokens) * d_model, output, output_len,
+                   static_cast<int>(n_tokens), static_cast<int>(n_heads),
+                   static_cast<int>(d_head), static_cast<int64_t>(d_model),
+                   static_cast<int>(t_past + 1));
+}
+
+int wrs_attn_prefill(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout* q_layout,
+                     int kv_dtype, const void* k, const wrs_layout* k_layout, const void* v,
+                     const wrs_layout* v_layout, float* out, const wrs_layout* out_layout,
+                     size_t batch, size_t n_heads, size_t t_q, size_t t_kv, size_t d_head,
+                     int causal, size_t q_pos_offset) {
+  if (!c) return WRS_EINVAL;
+  if (!q_layout || !k_layout || !v_layout || !out_layout)
+    return fail(c, WRS_EINVAL, "null layout");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  return prefill_impl(c, q_dtype, q, *q_layout, kv_dtype, k, *k_layout, v, *v_layout, out,
+                      *out_layout, batch, n_heads, t_q, t_kv, d_head, causal, q_pos_offset);
+}
+
+// ---------------------------------------------------------------- KV arena
+
+int wrs_kv_create(wrs_attn_ctx* c, size_t n_layers, size_t n_slots, size_t n_heads,
+                  size_t max_ctx, size_t n_audio_max, wrs_kv** out) {
+  if (!c || !out) return WRS_EINVAL;
+  *out = nullptr;
+  if (n_layers == 0 || n_heads == 0 || max_ctx == 0 || !fits_int(max_ctx) ||
+      !fits_int(n_audio_max) || !fits_int(n_slots))
+    return fail(c, WRS_EINVAL, "wrs_kv_create: bad geometry");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  auto* kv = new (std::nothrow) wrs_kv();
+  if (!kv) return WRS_ENOMEM;
+  kv->ctx = c;
+  kv->n_layers = n_layers;
+  kv->n_slots = n_slots;
+  kv->n_heads = n_heads;
+  kv->max_ctx = max_ctx;
+  kv->n_audio_max = n_audio_max;
+  kv->len.assign(n_slots, 0);
+  kv->cross_len.assign(n_layers, 0);
+  const size_t self_bytes = n_layers * n_slots * n_heads * max_ctx * 64 * 2;
+  const size_t cross_bytes = n_layers * n_heads * n_audio_max * 64 * 2;
+  bool ok = true;
+  if (self_bytes) {
+    ok = ok && hipMalloc(&kv->k_self, self_bytes) == hipSuccess;
+    ok = ok && hipMalloc(&kv->v_self, self_bytes) == hipSuccess;
+  }
+  if (cross_bytes) {
+    ok = ok && hipMalloc(&kv->k_cross, cross_bytes) == hipSuccess;
+    ok = ok && hipMalloc(&kv->v_cross, cross_bytes) == hipSuccess;
+  }
+  if (!ok) {
+    for (void* p : {(void*)kv->k_self, (void*)kv->v_self, (void*)kv->k_cross, (void*)kv->v_cross})
+      if (p) (void)hipFree(p);
+    delete kv;
+    return fail(c, WRS_ENOMEM, "wrs_kv_create: hipMalloc failed");
+  }
+  *out = kv;
+  return WRS_OK;
+}
+
+void wrs_kv_destroy(wrs_kv* kv) {
+  if (!kv) return;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (void* p : {(void*)kv->k_self, (void*)kv->v_self, (void*)kv->k_cross, (void*)kv->v_cross})
+    if (p) (void)hipFree(p);
+  delete kv;
+}
+
+int wrs_kv_clear(wrs_kv* kv) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  std::fill(kv->len.begin(), kv->len.end(), 0);
+  return WRS_OK;
+}
+
+int wrs_kv_clear_slot(wrs_kv* kv, size_t slot) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  if (slot >= kv->n_slots) return fail(kv->ctx, WRS_ERANGE, "slot out of range");
+  kv->len[slot] = 0;
+  return WRS_OK;
+}
+
+int wrs_kv_invalidate_cross(wrs_kv* kv) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  std::fill(kv->cross_len.begin(), kv->cross_len.end(), 0);
+  return WRS_OK;
+}
+
+int wrs_kv_ensure_slots(wrs_kv* kv, size_t n_slots) {
+  if (!kv) return WRS_EINVAL;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (n_slots <= kv->n_slots) return WRS_OK;
+  if (!fits_int(n_slots)) return fail(c, WRS_EINVAL, "n_slots exceeds 2^31");
+  DeviceGuard g(c->device);
+  const size_t slot_bytes = kv->n_heads * kv->plane() * 2;
+  const size_t bytes = kv->n_layers * n_slots * slot_bytes;
+  uint16_t *nk = nullptr, *nv = nullptr;
+  if (hipMalloc(&nk, bytes) != hipSuccess || hipMalloc(&nv, bytes) != hipSuccess) {
+    if (nk) (void)hipFree(nk);
+    return fail(c, WRS_ENOMEM, "wrs_kv_ensure_slots: hipMalloc failed");
+  }
+  if (kv->n_slots) {
+    const size_t w = kv->n_slots * slot_bytes;
+    WRS_HIP(c, hipMemcpy2DAsync(nk, n_slots * slot_bytes, kv->k_self, w, w, kv->n_layers,
+                                hipMemcpyDeviceToDevice, c->stream));
+    WRS_HIP(c, hipMemcpy2DAsync(nv, n_slots * slot_bytes, kv->v_self, w, w, kv->n_layers,
+                                hipMemcpyDeviceToDevice, c->stream));
+    WRS_HIP(c, hipStreamSynchronize(c->stream));
+    (void)hipFree(kv->k_self);
+    (void)hipFree(kv->v_self);
+  }
+  kv->k_self = nk;
+  kv->v_self = nv;
+  kv->n_slots = n_slots;
+  kv->len.resize(n_slots, 0);
+  return WRS_OK;
+}
+
+int wrs_kv_copy_slot(wrs_kv* kv, size_t dst, size_t src) {
+  if (!kv) return WRS_EINVAL;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (dst >= kv->n_slots || src >= kv->n_slots) return fail(c, WRS_ERANGE, "slot out of range");
+  if (dst == src) return WRS_OK;
+  DeviceGuard g(c->device);
+  const int64_t layer_stride = static_cast<int64_t>(kv->n_slots * kv->n_heads * kv->plane());
+  const int64_t plane = static_cast<int64_t>(kv->plane());
+  const int n = static_cast<int>(kv->len[src]);
+  auto* ks = reinterpret_cast<_Float16*>(kv->k_self);
+  auto* vs = reinterpret_cast<_Float16*>(kv->v_self);
+  WRS_HIP(c, wrs::launch_kv_copy_planes(ks + kv->self_off(0, src), ks + kv->self_off(0, dst),
+                                        layer_stride, plane, static_cast<int>(kv->n_layers),
+                                        static_cast<int>(kv->n_heads), n, c->stream));
+  WRS_HIP(c, wrs::launch_kv_copy_planes(vs + kv->self_off(0, src), vs + kv->self_off(0, dst),
+                                        layer_stride, plane, static_cast<int>(kv->n_layers),
+                                        static_cast<int>(kv->n_heads), n, c->stream));
+  kv->len[dst] = kv->len[src];
+  return WRS_OK;
+}
+
+int wrs_kv_slot_len(wrs_kv* kv, size_t slot, size_t* len) {
+  if (!kv || !len) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  if (slot >= kv->n_slots) return fail(kv->ctx, WRS_ERANGE, "slot out of range");
+  *len = kv->len[slot];
+  return WRS_OK;
+}
+
+int wrs_kv_set_len(wrs_kv* kv, size_t slot, size_t len) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  if (slot >= kv->n_slots) return fail(kv->ctx, WRS_ERANGE, "slot out of range");
+  if (len > kv->len[slot])
+    return fail(kv->ctx, WRS_EINVAL, "set_len: rows beyond the stored history do not exist");
+  kv->len[slot] = len;
+  return WRS_OK;
+}
+
+int wrs_kv_slide_to_fit(wrs_kv* kv, size_t slot, size_t n_new, size_t max_ctx, size_t* pos) {
+  if (!kv) return WRS_EINVAL;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (slot >= kv->n_slots) return fail(c, WRS_ERANGE, "slot out of range");
+  size_t t_past = kv->len[slot];
+  if (t_past + n_new > max_ctx) {  // decoder.rs:250-261
+    const size_t drop = std::min(t_past + n_new - max_ctx, t_past);
+    DeviceGuard g(c->device);
+    const int64_t layer_stride = static_cast<int64_t>(kv->n_slots * kv->n_heads * kv->plane());
+    const int64_t plane = static_cast<int64_t>(kv->plane());
+    auto* ks = reinterpret_cast<_Float16*>(kv->k_self);
+    auto* vs = reinterpret_cast<_Float16*>(kv->v_self);
+    WRS_HIP(c, wrs::launch_kv_slide(ks + kv->self_off(0, slot), layer_stride, plane,
+                                    static_cast<int>(kv->n_layers), static_cast<int>(kv->n_heads),
+                                    static_cast<int>(t_past), static_cast<int>(drop), c->stream));
+    WRS_HIP(c, wrs::launch_kv_slide(vs + kv->self_off(0, slot), layer_stride, plane,
+                                    static_cast<int>(kv->n_layers), static_cast<int>(kv->n_heads),
+                                    static_cast<int>(t_past), static_cast<int>(drop), c->stream));
+    t_past -= drop;
+    kv->len[slot] = t_past;
+  }
+  if (pos) *pos = t_past;
+  return WRS_OK;
+}
+
+int wrs_kv_append(wrs_kv* kv, size_t layer, size_t slot, const float* k_rows,
+                  const float* v_rows, size_t n, int src_on_host) {
+  if (!kv) return WRS_EINVAL;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers || slot >= kv->n_slots) return fail(c, WRS_ERANGE, "layer/slot out of range");
+  if (n == 0) return WRS_OK;
+  if (!k_rows || !v_rows) return fail(c, WRS_EINVAL, "null rows");
+  const size_t pos = kv->len[slot];
+  if (pos + n > kv->max_ctx) return fail(c, WRS_ERANGE, "append past the arena's max_ctx");
+  DeviceGuard g(c->device);
+  const size_t floats = n * kv->d_model();
+  int rc = WRS_OK;
+  if (src_on_host) {
+    rc = grow(c, &c->stage, &c->stage_bytes, 2 * align_up(floats * 4, 256), false);
+    if (rc) return rc;
+  }
+  const float* dk = to_device_f32(c, k_rows, floats, src_on_host, 0, &rc);
+  if (rc) return rc;
+  const float* dv = to_device_f32(c, v_rows, floats, src_on_host, align_up(floats * 4, 256), &rc);
+  if (rc) return rc;
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  const int64_t plane = static_cast<int64_t>(kv->plane());
+  auto* ks = reinterpret_cast<_Float16*>(kv->k_self) + kv->self_off(layer, slot);
+  auto* vs = reinterpret_cast<_Float16*>(kv->v_self) + kv->self_off(layer, slot);
+  WRS_HIP(c, wrs::launch_kv_write_rows(dk, dm, static_cast<int>(n), static_cast<int>(kv->n_heads),
+                                       ks, plane, static_cast<int>(pos), c->stream));
+  WRS_HIP(c, wrs::launch_kv_write_rows(dv, dm, static_cast<int>(n), static_cast<int>(kv->n_heads),
+                                       vs, plane, static_cast<int>(pos), c->stream));
+  if (src_on_host) WRS_HIP(c, hipStreamSynchronize(c->stream));
+  return WRS_OK;
+}
+
+int wrs_kv_advance(wrs_kv* kv, size_t slot, size_t n) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  if (slot >= kv->n_slots) return fail(kv->ctx, WRS_ERANGE, "slot out of range");
+  if (kv->len[slot] + n > kv->max_ctx) return fail(kv->ctx, WRS_ERANGE, "advance past max_ctx");
+  kv->len[slot] += n;
+  return WRS_OK;
+}
+
+int wrs_kv_set_cross(wrs_kv* kv, size_t layer, const float* k, const float* v, size_t n_audio,
+                     int src_on_host) {
+  if (!kv) return WRS_EINVAL;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n_audio > kv->n_audio_max) return fail(c, WRS_ERANGE, "n_audio exceeds the arena");
+  if (n_audio && (!k || !v)) return fail(c, WRS_EINVAL, "null rows");
+  DeviceGuard g(c->device);
+  const size_t floats = n_audio * kv->d_model();
+  int rc = WRS_OK;
+  if (src_on_host && floats) {
+    rc = grow(c, &c->stage, &c->stage_bytes, 2 * align_up(floats * 4, 256), false);
+    if (rc) return rc;
+  }
+  if (floats) {
+    const float* dk = to_device_f32(c, k, floats, src_on_host, 0, &rc);
+    if (rc) return rc;
+    const float* dv = to_device_f32(c, v, floats, src_on_host, align_up(floats * 4, 256), &rc);
+    if (rc) return rc;
+    const int64_t dm = static_cast<int64_t>(kv->d_model());
+    const int64_t plane = static_cast<int64_t>(kv->n_audio_max * 64);
+    auto* kc = reinterpret_cast<_Float16*>(kv->k_cross) + kv->cross_off(layer);
+    auto* vc = reinterpret_cast<_Float16*>(kv->v_cross) + kv->cross_off(layer);
+    WRS_HIP(c, wrs::launch_kv_write_rows(dk, dm, static_cast<int>(n_audio),
+                                         static_cast<int>(kv->n_heads), kc, plane, 0, c->stream));
+    WRS_HIP(c, wrs::launch_kv_write_rows(dv, dm, static_cast<int>(n_audio),
+                                         static_cast<int>(kv->n_heads), vc, plane, 0, c->stream));
+    if (src_on_host) WRS_HIP(c, hipStreamSynchronize(c->stream));
+  }
+  kv->cross_len[layer] = n_audio;
+  return WRS_OK;
+}
+
+int wrs_kv_cross_len(wrs_kv* kv, size_t* n_audio) {
+  if (!kv || !n_audio) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  *n_audio = kv->cross_len.empty() ? 0 : kv->cross_len[0];
+  return WRS_OK;
+}
+
+int wrs_kv_self_planes(wrs_kv* kv, void** k, void** v, size_t* slot_stride_elems) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  if (k) *k = kv->k_self;
+  if (v) *v = kv->v_self;
+  if (slot_stride_elems) *slot_stride_elems = kv->n_heads * kv->plane();
+  return WRS_OK;
+}
+
+int wrs_kv_cross_planes(wrs_kv* kv, void** k, void** v) {
+  if (!kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(kv->ctx->mu);
+  if (k) *k = kv->k_cross;
+  if (v) *v = kv->v_cross;
+  return WRS_OK;
+}
+
+int wrs_attn_decode_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const size_t* slots,
+                         size_t n, const float* q, float* out) {
+  if (!c || !kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n == 0) return WRS_OK;
+  if (!slots || !q || !out) return fail(c, WRS_EINVAL, "null argument");
+  DeviceGuard g(c->device);
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  for (size_t i0 = 0; i0 < n; i0 += wrs::kMaxDecodeGroups) {
+    const size_t m = std::min<size_t>(wrs::kMaxDecodeGroups, n - i0);
+    std::vector<int64_t> goff(m);
+    std::vector<int> lens(m);
+    for (size_t i = 0; i < m; ++i) {
+      const size_t s = slots[i0 + i];
+      if (s >= kv->n_slots) return fail(c, WRS_ERANGE, "slot out of range");
+      // The step's own row sits at position len (appended, not yet advanced).
+      if (kv->len[s] + 1 > kv->max_ctx) return fail(c, WRS_ERANGE, "slot is full");
+      goff[i] = static_cast<int64_t>(kv->self_off(layer, s));
+      lens[i] = static_cast<int>(kv->len[s] + 1);
+    }
+    int rc = decode_impl(c, q + i0 * dm, dm, out + i0 * dm, dm, kv->k_self, kv->v_self,
+                         static_cast<int64_t>(kv->plane()), goff, lens, 1,
+                         static_cast<int>(kv->n_heads));
+    if (rc) return rc;
+  }
+  return WRS_OK;
+}
+
+int wrs_attn_decode_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                          size_t n_beams, float* out) {
+  if (!c || !kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n_beams == 0) return WRS_OK;
+  if (!q || !out) return fail(c, WRS_EINVAL, "null argument");
+  DeviceGuard g(c->device);
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  const size_t L = kv->cross_len[layer];
+  // All beams of the utterance share one read of the plane; beyond 8 beams the
+  // rows go in further launches of up to 8.
+  for (size_t b0 = 0; b0 < n_beams; b0 += wrs::kMaxRowsPerGroup) {
+    const size_t rows = std::min<size_t>(wrs::kMaxRowsPerGroup, n_beams - b0);
+    std::vector<int64_t> goff(1, static_cast<int64_t>(kv->cross_off(layer)));
+    std::vector<int> lens(1, static_cast<int>(L));
+    int rc = decode_impl(c, q + b0 * dm, dm, out + b0 * dm, dm, kv->k_cross, kv->v_cross,
+                         static_cast<int64_t>(kv->n_audio_max * 64), goff, lens,
+                         static_cast<int>(rows), static_cast<int>(kv->n_heads));
+    if (rc) return rc;
+  }
+  return WRS_OK;
+}
+
+int wrs_attn_prefill_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, size_t slot, const float* q,
+                          size_t n_tokens, float* out) {
+  if (!c || !kv) return WRS_EINVAL;
+  if (n_tokens == 1) return wrs_attn_decode_self(c, kv, layer, &slot, 1, q, out);
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers || slot >= kv->n_slots) return fail(c, WRS_ERANGE, "layer/slot out of range");
+  if (n_tokens == 0) return WRS_OK;
+  const size_t t_past = kv->len[slot];
+  if (t_past + n_tokens > kv->max_ctx) return fail(c, WRS_ERANGE, "rows past max_ctx");
+  DeviceGuard g(c->device);
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  const wrs_layout lq{0, 64, dm};
+  const wrs_layout lkv{0, static_cast<int64_t>(kv->plane()), 64};
+  const uint16_t* kb = kv->k_self + kv->self_off(layer, slot);
+  const uint16_t* vb = kv->v_self + kv->self_off(layer, slot);
+  return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
+                      n_tokens, t_past + n_tokens, 64, 1, t_past);
+}
+
+int wrs_attn_prefill_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                           size_t n_tokens, float* out) {
+  if (!c || !kv) return WRS_EINVAL;
+  if (n_tokens == 1) return wrs_attn_decode_cross(c, kv, layer, q, 1, out);
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n_tokens == 0) return WRS_OK;
+  DeviceGuard g(c->device);
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  const wrs_layout lq{0, 64, dm};
+  const wrs_layout lkv{0, static_cast<int64_t>(kv->n_audio_max * 64), 64};
+  const uint16_t* kb = kv->k_cross + kv->cross_off(layer);
+  const uint16_t* vb = kv->v_cross + kv->cross_off(layer);
+  return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
+                      n_tokens, kv->cross_len[layer], 64, 0, 0);
+}
+
+}  // extern "C"

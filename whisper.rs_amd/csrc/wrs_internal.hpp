@@ -1,0 +1,99 @@
+// Internal declarations shared by the HIP kernels and the C-ABI runtime.
+//
+// Layout conventions (all strides in elements, not bytes):
+//   activations  element (b, h, t, d) at base + b*bs + h*hs + t*rs + d
+//                (token-major [T][n_heads*d_head] rows of the reference are
+//                 hs = d_head, rs = d_model; BHSD is hs = T*d_head, rs = d_head)
+//   KV cache     f16, one [ctx][64] plane per (layer, slot, head) -- rows of
+//                one head are contiguous 128-byte lines.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wrs {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+struct Layout {
+  int64_t bs;  // batch (window) stride
+  int64_t hs;  // head stride
+  int64_t rs;  // row (token) stride
+};
+
+// Flash-attention prefill over full query/key sequences
+// (crates/tensor/src/ops/attention.rs:68-243 semantics).
+struct PrefillArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  float* o;
+  Layout lq, lk, lv, lo;
+  int batch, n_heads, t_q, t_kv, d_head;
+  int causal;        // mask keys j > i + q_pos_offset
+  int q_pos_offset;  // absolute position of query row 0 (decoder prompt: t_past)
+  float scale;       // 1/sqrt(d_head), rounded to f32 like attention.rs:107
+};
+
+// MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type.
+hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s);
+// f32-accumulate-check kernel on f32 MFMA: q f32, k/v f32|f16|bf16 widened
+// exactly to f32, any d_head <= 128.
+hipError_t launch_prefill_f32(const PrefillArgs& a, DType q_dt, DType kv_dt, hipStream_t s);
+
+// Exact reference decode semantics for f32 host-slice calls
+// (attention.rs:246-434 single_token_mha_d64 and decoder.rs:835-892):
+// full score row, softmax with reciprocal multiply, weights < 1e-7 skipped.
+// Row i sees keys [0, row_limit0 + i) (row_limit0 = t_kv for single-token).
+struct ExactArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t q_rs, kv_rs, o_rs;  // row strides (d_model)
+  int n_rows, n_heads, d_head;
+  int row_limit0;
+  float scale;
+  float* scores;  // scratch [n_rows][n_heads][scores_stride]
+  int64_t scores_stride;
+};
+hipError_t launch_decode_exact_f32(const ExactArgs& a, hipStream_t s);
+
+// Split-K decode over an f16 KV cache: one query row per (group, row),
+// all rows of a group share one K/V plane set (cross-attention: the beams of
+// one utterance; self-attention: one row per slot).
+constexpr int kMaxDecodeGroups = 64;
+constexpr int kMaxRowsPerGroup = 8;
+struct DecodeArgs {
+  const float* q;   // row (g*rows_per_group + r): q + row*q_rs + h*64
+  float* o;         // same indexing with o_rs
+  const _Float16* k;  // plane (g, h): k + goff[g] + h*kv_hs, key j at +j*64
+  const _Float16* v;
+  int64_t q_rs, o_rs, kv_hs;
+  int64_t goff[kMaxDecodeGroups];  // per-group plane offset (elements)
+  int len[kMaxDecodeGroups];       // keys visible to group g
+  int n_groups, rows_per_group, n_heads;
+  int chunk;     // keys per workgroup
+  int n_splits;  // workgroups per (group, head)
+  float scale_log2;  // (1/8) * log2(e)
+  float* part;        // scratch: [groups][heads][splits][rows][66]
+  unsigned* counters;  // scratch: [groups][heads], zero between launches
+};
+hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s);
+size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows);
+
+// KV arena kernels.
+// f32 rows [n][d_model] (row stride src_rs) -> f16 planes: head h, row i at
+// dst + h*dst_hs + (pos + i)*64.
+hipError_t launch_kv_write_rows(const float* src, int64_t src_rs, int n, int n_heads,
+                                _Float16* dst, int64_t dst_hs, int pos, hipStream_t s);
+// Planes of one slot: plane (l, h) at base + l*layer_stride + h*plane_stride.
+// Move rows [drop, len) of every plane down to [0, len - drop).
+hipError_t launch_kv_slide(_Float16* base, int64_t layer_stride, int64_t plane_stride,
+                           int n_layers, int n_heads, int len, int drop, hipStream_t s);
+// Copy rows [0, len) of every plane from src to dst (same plane geometry).
+hipError_t launch_kv_copy_planes(const _Float16* src, _Float16* dst, int64_t layer_stride,
+                                 int64_t plane_stride, int n_layers, int n_heads, int len,
+                                 hipStream_t s);
+
+}  // namespace wrs
