@@ -3,15 +3,20 @@
 // K2 (decode_f16): split-K attention over the f16 KV cache
 //   (replaces crates/tensor/src/ops/attention.rs:246-434 single_token_mha_d64
 //    as called from crates/whisper/src/decoder.rs:636 / :698).
-//   Grid (split, head, group). A workgroup owns `chunk` = 64 consecutive keys
+//   Grid (split, head, group). A workgroup owns kChunk = 128 consecutive keys
 //   of one (group, head) plane and ALL query rows of the group (the beams of
 //   an utterance share the cross-attention plane, so it is read once per step
-//   instead of once per beam). Each thread issues its K and V loads (2 x 16 B
-//   each) before any arithmetic, so the whole layer's cache is in flight from
-//   the first cycle. Partial (max, sum, acc[64]) per row go to scratch; the
-//   last workgroup of a (group, head) to finish -- detected with an
-//   agent-scope counter -- merges them with the log-sum-exp rule and writes
-//   the output, then re-arms the counter for the next launch.
+//   instead of once per beam). Every thread issues its q load and all its K and
+//   V loads (2 keys x 2 x 16 B each) before any arithmetic, so the whole
+//   layer's cache is in flight from the first cycles.
+//   Partials (max, sum, acc[64]) per row are published with agent-scope
+//   (sc1, L2-coherent) stores; after every wave has waited for its stores, one
+//   thread bumps the (group, head) counter -- each on its own 128-byte line, so
+//   the increments of different heads do not serialize. The workgroup that
+//   sees the last count merges all splits with the log-sum-exp rule, reading
+//   the partials with agent-scope loads issued 16 at a time, writes the output
+//   and re-arms its counter. Agent-scope atomics avoid the full-L2 writeback
+//   and invalidate that a device-wide __threadfence costs on gfx950.
 //
 // decode_exact_f32: the reference's own decode arithmetic on f32 K/V for the
 //   host-slice entry points: full score row, max, exp, sum, reciprocal
@@ -26,19 +31,44 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 64;  // keys per workgroup (4 threads per key)
-constexpr int kPart = 66;   // floats per partial row: m, l, acc[64]
+constexpr int kChunk = kDecodeChunk;  // keys per workgroup: 2 per thread, 4 threads per key
+constexpr int kKpt = kChunk / 64;
+constexpr int kPart = 68;    // floats per partial row: m, l, 2 pad, acc[64]
+constexpr int kCounterStride = 32;  // 128 bytes between merge counters
+constexpr int kMergeBatch = 16;     // partial loads in flight per thread
 
+// Cross-lane moves inside a row of 16 lanes (DPP): xor 1, xor 2, mirror-8, mirror-16.
+template <int CTRL>
+__device__ inline float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                0xF, 0xF, false));
+}
+__device__ inline float quad_sum(float x) {
+  x += dpp<0xB1>(x);
+  return x + dpp<0x4E>(x);
+}
 __device__ inline float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ inline float wave_sum(float x) {
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  x += dpp<0x141>(x);
+  x += dpp<0x140>(x);
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
 }
 
-__device__ inline float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+__device__ inline void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int R>
@@ -54,64 +84,81 @@ __global__ __launch_bounds__(kThreads) void decode_f16(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int rows = a.rows_per_group;
   const int len = a.len[g];
-  const int k_lo = split * kChunk;
+  const int part = tid & 3, kl0 = tid >> 2;
 
-  // Issue every cache load of this workgroup first.
-  const int kl = tid >> 2, part = tid & 3;
-  const int key = k_lo + kl;
-  const bool valid = key < len;
-  const _Float16* kp = a.k + a.goff[g] + h * a.kv_hs + static_cast<int64_t>(key) * 64 + part * 16;
-  const _Float16* vp = a.v + a.goff[g] + h * a.kv_hs + static_cast<int64_t>(key) * 64 + part * 16;
-  u32x4 k0 = {0, 0, 0, 0}, k1 = {0, 0, 0, 0}, v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
-  if (valid) {
-    k0 = *reinterpret_cast<const u32x4*>(kp);
-    k1 = *reinterpret_cast<const u32x4*>(kp + 8);
-    v0 = *reinterpret_cast<const u32x4*>(vp);
-    v1 = *reinterpret_cast<const u32x4*>(vp + 8);
+  // Query rows of this head first (row tid/64 and row tid/64 + 4), then every
+  // cache load of the workgroup.
+  const int qr = tid >> 6, qd = tid & 63;
+  const float* qbase = a.q + static_cast<int64_t>(g * rows) * a.q_rs + h * 64 + qd;
+  float qv0 = 0.f, qv1 = 0.f;
+  if (qr < rows) qv0 = qbase[static_cast<int64_t>(qr) * a.q_rs];
+  if (R > 4 && qr + 4 < rows) qv1 = qbase[static_cast<int64_t>(qr + 4) * a.q_rs];
+  u32x4 kx[kKpt][2], vx[kKpt][2];
+  const _Float16* kplane = a.k + a.goff[g] + h * a.kv_hs;
+  const _Float16* vplane = a.v + a.goff[g] + h * a.kv_hs;
+#pragma unroll
+  for (int i = 0; i < kKpt; ++i) {
+    const int key = split * kChunk + kl0 + 64 * i;
+    if (key < len) {
+      const _Float16* kp = kplane + static_cast<int64_t>(key) * 64 + part * 16;
+      const _Float16* vp = vplane + static_cast<int64_t>(key) * 64 + part * 16;
+      kx[i][0] = *reinterpret_cast<const u32x4*>(kp);
+      kx[i][1] = *reinterpret_cast<const u32x4*>(kp + 8);
+      vx[i][0] = *reinterpret_cast<const u32x4*>(vp);
+      vx[i][1] = *reinterpret_cast<const u32x4*>(vp + 8);
+    } else {
+      kx[i][0] = kx[i][1] = vx[i][0] = vx[i][1] = u32x4{0, 0, 0, 0};
+    }
   }
-
-  // Queries of the group, pre-scaled so scores come out in the exp2 domain.
-  for (int e = tid; e < R * 64; e += kThreads) {
-    const int r = e >> 6, d = e & 63;
-    float x = 0.f;
-    if (r < rows)
-      x = a.q[static_cast<int64_t>(g * rows + r) * a.q_rs + h * 64 + d] * a.scale_log2;
-    qs[r][d] = x;
-  }
+  if (qr < R) qs[qr][qd] = qv0 * a.scale_log2;  // rows >= `rows` hold zeros
+  if (R > 4 && qr + 4 < R) qs[qr + 4][qd] = qv1 * a.scale_log2;
   __syncthreads();
 
-  // Scores: 16-wide partial dot per thread, reduced over the 4 threads of a key.
-  {
-    const f16x8 ka = __builtin_bit_cast(f16x8, k0);
-    const f16x8 kb = __builtin_bit_cast(f16x8, k1);
+  // Scores in the exp2 domain: 16-wide partial dots, summed over the 4 lanes
+  // of a key with DPP.
+#pragma unroll
+  for (int i = 0; i < kKpt; ++i) {
+    const int kl = kl0 + 64 * i;
+    const bool valid = split * kChunk + kl < len;
+    const f16x8 ka = __builtin_bit_cast(f16x8, kx[i][0]);
+    const f16x8 kb = __builtin_bit_cast(f16x8, kx[i][1]);
     float kf[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kf[i] = static_cast<float>(ka[i]);
-      kf[8 + i] = static_cast<float>(kb[i]);
+    for (int j = 0; j < 8; ++j) {
+      kf[j] = static_cast<float>(ka[j]);
+      kf[8 + j] = static_cast<float>(kb[j]);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float s = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s = __builtin_fmaf(qs[r][part * 16 + i], kf[i], s);
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
+      for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qs[r][part * 16 + j], kf[j], s);
+      s = quad_sum(s);
       if (part == 0) ps[r][kl] = valid ? s : -INFINITY;
     }
+    *reinterpret_cast<u32x4*>(&vs[kl][part * 16]) = vx[i][0];
+    *reinterpret_cast<u32x4*>(&vs[kl][part * 16 + 8]) = vx[i][1];
   }
-  *reinterpret_cast<u32x4*>(&vs[kl][part * 16]) = v0;
-  *reinterpret_cast<u32x4*>(&vs[kl][part * 16 + 8]) = v1;
   __syncthreads();
 
-  // Softmax statistics of this chunk: one wave per row.
+  // Chunk softmax statistics: one wave per row.
   const int wave = tid >> 6, lane = tid & 63;
   for (int r = wave; r < R; r += 4) {
-    const float x = ps[r][lane];
-    const float mx = wave_max(x);
-    const float p = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x - mx);
-    const float sum = wave_sum(p);
-    ps[r][lane] = p;
+    float x[kKpt], mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kKpt; ++i) {
+      x[i] = ps[r][lane + 64 * i];
+      mx = fmaxf(mx, x[i]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kKpt; ++i) {
+      const float p = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[i] - mx);
+      ps[r][lane + 64 * i] = p;
+      sum += p;
+    }
+    sum = wave_sum(sum);
     if (lane == 0) {
       mrow[r] = mx;
       lrow[r] = sum;
@@ -119,15 +166,15 @@ __global__ __launch_bounds__(kThreads) void decode_f16(DecodeArgs a) {
   }
   __syncthreads();
 
-  // P V over the chunk: thread (quarter, d) sums 16 keys for every row.
+  // P V over the chunk: thread (quarter, d) sums 32 keys for every row.
   {
     const int d = tid & 63, qq = tid >> 6;
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kk = qq * 16 + i;
+#pragma unroll 8
+    for (int i = 0; i < kChunk / 4; ++i) {
+      const int kk = qq * (kChunk / 4) + i;
       const float vv = static_cast<float>(vs[kk][d]);
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = __builtin_fmaf(ps[r][kk], vv, acc[r]);
@@ -138,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void decode_f16(DecodeArgs a) {
   __syncthreads();
 
   if (a.n_splits == 1) {
-    // Whole row in one workgroup: normalize and store directly.
+    // The whole row in one workgroup: normalize and store directly.
     for (int e = tid; e < rows * 64; e += kThreads) {
       const int r = e >> 6, d = e & 63;
       const float v = red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d];
@@ -152,39 +199,62 @@ __global__ __launch_bounds__(kThreads) void decode_f16(DecodeArgs a) {
   float* mine = a.part + (static_cast<int64_t>(gh) * a.n_splits + split) * rows * kPart;
   for (int e = tid; e < rows * 64; e += kThreads) {
     const int r = e >> 6, d = e & 63;
-    mine[r * kPart + 2 + d] = red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d];
+    st_agent(mine + r * kPart + 4 + d, red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d]);
   }
   if (tid < rows) {
-    mine[tid * kPart] = mrow[tid];
-    mine[tid * kPart + 1] = lrow[tid];
+    st_agent(mine + tid * kPart, mrow[tid]);
+    st_agent(mine + tid * kPart + 1, lrow[tid]);
   }
-  __threadfence();
+  // Every wave waits until its agent-scope stores are performed, so the
+  // counter increment below is ordered after all of this workgroup's partials.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  unsigned* counter = a.counters + gh * kCounterStride;
   if (tid == 0) {
-    const unsigned done = atomicAdd(a.counters + gh, 1u);
+    const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
     last_flag = (done == static_cast<unsigned>(a.n_splits - 1));
   }
   __syncthreads();
   if (!last_flag) return;
-  __threadfence();
 
-  // Log-sum-exp merge of all splits (values are in the exp2 domain).
+  // Log-sum-exp merge of all splits (exp2 domain), batches of kMergeBatch
+  // splits with their loads issued together, folded online across batches.
   const float* base = a.part + static_cast<int64_t>(gh) * a.n_splits * rows * kPart;
   for (int e = tid; e < rows * 64; e += kThreads) {
     const int r = e >> 6, d = e & 63;
-    float M = -INFINITY;
-    for (int sp = 0; sp < a.n_splits; ++sp) M = fmaxf(M, base[(sp * rows + r) * kPart]);
-    float L = 0.f, acc = 0.f;
-    for (int sp = 0; sp < a.n_splits; ++sp) {
-      const float* pr = base + (sp * rows + r) * kPart;
-      const float ms = pr[0];
-      const float w = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-      L = __builtin_fmaf(pr[1], w, L);
-      acc = __builtin_fmaf(pr[2 + d], w, acc);
+    float M = -INFINITY, L = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < a.n_splits; s0 += kMergeBatch) {
+      float ms[kMergeBatch], ls[kMergeBatch], as[kMergeBatch];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        ms[j] = -INFINITY;
+        ls[j] = as[j] = 0.f;
+        if (s0 + j < a.n_splits) {
+          const float* pr = base + ((s0 + j) * rows + r) * kPart;
+          ms[j] = ld_agent(pr);
+          ls[j] = ld_agent(pr + 1);
+          as[j] = ld_agent(pr + 4 + d);
+        }
+      }
+      float Mb = M;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, ms[j]);
+      if (Mb == -INFINITY) continue;
+      const float scale = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mb);
+      L *= scale;
+      acc *= scale;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const float w = (ms[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[j] - Mb);
+        L = __builtin_fmaf(ls[j], w, L);
+        acc = __builtin_fmaf(as[j], w, acc);
+      }
+      M = Mb;
     }
     a.o[static_cast<int64_t>(g * rows + r) * a.o_rs + h * 64 + d] = L > 0.f ? acc * (1.f / L) : 0.f;
   }
-  if (tid == 0) a.counters[gh] = 0u;
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ inline float block_reduce(float x, float* sh, bool is_max) {
@@ -255,6 +325,10 @@ __global__ __launch_bounds__(kThreads) void decode_exact_f32(ExactArgs a) {
 
 size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows) {
   return static_cast<size_t>(n_groups) * n_heads * n_splits * rows * kPart;
+}
+
+size_t decode_counter_words(int n_groups, int n_heads) {
+  return static_cast<size_t>(n_groups) * n_heads * kCounterStride;
 }
 
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s) {

@@ -240,8 +240,8 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
   a.n_groups = n_groups;
   a.rows_per_group = rows_per_group;
   a.n_heads = n_heads;
-  a.chunk = 64;
-  a.n_splits = std::max(1, (max_len + 63) / 64);
+  a.chunk = wrs::kDecodeChunk;
+  a.n_splits = std::max(1, (max_len + wrs::kDecodeChunk - 1) / wrs::kDecodeChunk);
   a.scale_log2 = 0.125f * 1.4426950408889634f;
   if (a.n_splits > 1) {
     const size_t pb =
@@ -249,7 +249,7 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
     int rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes, pb, false);
     if (rc) return rc;
     rc = grow(c, reinterpret_cast<void**>(&c->counters), &c->counter_bytes,
-              static_cast<size_t>(n_groups) * n_heads * sizeof(unsigned), true);
+              wrs::decode_counter_words(n_groups, n_heads) * sizeof(unsigned), true);
     if (rc) return rc;
   }
   a.part = c->part;

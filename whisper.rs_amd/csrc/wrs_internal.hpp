@@ -73,14 +73,16 @@ struct DecodeArgs {
   int64_t goff[kMaxDecodeGroups];  // per-group plane offset (elements)
   int len[kMaxDecodeGroups];       // keys visible to group g
   int n_groups, rows_per_group, n_heads;
-  int chunk;     // keys per workgroup
-  int n_splits;  // workgroups per (group, head)
+  int chunk;     // keys per workgroup (kDecodeChunk)
+  int n_splits;  // workgroups per (group, head) = ceil(max len / chunk)
   float scale_log2;  // (1/8) * log2(e)
-  float* part;        // scratch: [groups][heads][splits][rows][66]
-  unsigned* counters;  // scratch: [groups][heads], zero between launches
+  float* part;        // scratch: [groups][heads][splits][rows][68]
+  unsigned* counters;  // scratch: one per (group, head) every 32 words, zero between launches
 };
+constexpr int kDecodeChunk = 128;
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s);
 size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows);
+size_t decode_counter_words(int n_groups, int n_heads);
 
 // KV arena kernels.
 // f32 rows [n][d_model] (row stride src_rs) -> f16 planes: head h, row i at
