@@ -193,6 +193,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--only", choices=["encoder", "decode"], default=None,
+                    help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -207,6 +209,14 @@ def main():
     ctx.use_torch_stream()
     props = torch.cuda.get_device_properties(0)
 
+    if args.only == "encoder":
+        _, ms, tflops, _ = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
+        log(f"encoder only: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s")
+        return
+    if args.only == "decode":
+        _, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
+        log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
+        return
     cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
     copy_gbs = copy_bandwidth()
