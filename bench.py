@@ -22,7 +22,11 @@ import argparse
 import importlib.util
 import json
 import os
+import shutil
+import sqlite3
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -78,7 +82,7 @@ def bench_encoder(wrs, W, ctx, steps, warmup):
     return cfg, ms, tflops, (q, k, v)
 
 
-def bench_decode(wrs, W, ctx, reps):
+def bench_decode(wrs, W, ctx, reps, use_graph=True):
     import torch
     cfg = W.LARGE_CROSS_DECODE
     U = 3  # utterances rotated: 3 x 245.76 MB of cross K/V > 256 MB MALL
@@ -100,6 +104,13 @@ def bench_decode(wrs, W, ctx, reps):
 
     all_layers()  # sizes the scratch outside any capture
     torch.cuda.synchronize()
+    if not use_graph:  # eager launches (counter passes)
+        for _ in range(reps):
+            all_layers()
+        torch.cuda.synchronize()
+        for ar in arenas:
+            ar.close()
+        return cfg, float("nan"), float("nan")
     eager = outs.clone()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
@@ -144,6 +155,57 @@ def copy_bandwidth():
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / 10
     return 2 * a.numel() * 4 / (ms * 1e-3) / 1e9
+
+
+CALIB_BYTES = 256 << 20  # one plain device copy of this many bytes per profiled run
+
+
+def calibration_copy():
+    """A plain copy of known size: the reference point for FETCH_SIZE/WRITE_SIZE."""
+    import torch
+    a = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def measure_traffic(only: str, kernel_tag: str, extra: list[str]):
+    """HBM bytes per launch of the kernel whose name contains kernel_tag.
+
+    Two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch)
+    over `bench.py --only <only>`; each counter is scaled by what it reads for
+    the plain copy of CALIB_BYTES in the same run. Returns None when rocprofv3
+    is unavailable or a pass fails.
+    """
+    if shutil.which("rocprofv3") is None:
+        return None
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory(dir="/tmp") as d:
+            cmd = ["timeout", "-s", "KILL", "150", "rocprofv3", "--pmc", counter, "-d", d, "-o",
+                   "t", "--", sys.executable, str(Path(__file__).resolve()), "--only", only] + extra
+            env = dict(os.environ, TMPDIR="/tmp")
+            r = subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, env=env,
+                               cwd="/tmp")
+            dbs = list(Path(d).rglob("*_results.db"))
+            if r.returncode != 0 or not dbs:
+                log(f"traffic: {counter} pass failed (rc={r.returncode})")
+                return None
+            db = sqlite3.connect(str(dbs[0]))
+            rows = db.execute("select kernel_name, avg(value) from counters_collection "
+                              "where counter_name = ? group by kernel_name", (counter,)).fetchall()
+            db.close()
+            kern = [v for n, v in rows if kernel_tag in n]
+            copy = [v for n, v in rows if "copy" in n.lower() or "elementwise" in n.lower()]
+            if not kern or not copy or max(copy) <= 0:
+                log(f"traffic: {counter}: kernels not found in the profile")
+                return None
+            factor = CALIB_BYTES / (max(copy) * 1024.0)
+            out[counter] = kern[0] * 1024.0 * factor
+            out[counter + "_factor"] = factor
+            log(f"traffic: {only} {counter} = {kern[0]:.1f} KiB/dispatch, copy of "
+                f"{CALIB_BYTES} B reads {max(copy):.1f} KiB -> factor {factor:.4f}")
+    return out
 
 
 def cpu_baseline_encoder(cfg, qkv, threads):
@@ -193,6 +255,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --only decode: plain launches instead of a graph replay")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 HBM-traffic passes")
     ap.add_argument("--only", choices=["encoder", "decode"], default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
@@ -211,15 +277,26 @@ def main():
 
     if args.only == "encoder":
         _, ms, tflops, _ = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
+        calibration_copy()
         log(f"encoder only: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s")
         return
     if args.only == "decode":
-        _, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
+        _, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps, use_graph=not args.eager)
+        calibration_copy()
         log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
         return
     cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
     copy_gbs = copy_bandwidth()
+
+    enc_traffic = dec_traffic = None
+    if not args.no_traffic:
+        log("traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes")
+        enc_traffic = measure_traffic("encoder", "fa2_prefill", ["--steps", "3", "--warmup", "1"])
+        dec_traffic = measure_traffic("decode", "decode_f16", ["--decode-reps", "3", "--eager"])
+
+    def traffic_bytes(t):
+        return None if t is None else round(t["FETCH_SIZE"] + t["WRITE_SIZE"])
 
     threads = min(16, os.cpu_count() or 1)
     cpu_enc = cpu_dec = None
@@ -246,14 +323,15 @@ def main():
                    "frames": cfg.t, "d_head": 64, "flops_per_step": cfg.flops()},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": traffic_bytes(enc_traffic)},
         "cpu_baseline": cpu_enc,
         "decode_cross": {
             "workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s",
             "us_per_launch": round(us, 3), "launches_per_step": dcfg.n_layers,
             "bytes_per_launch": dcfg.bytes_per_layer(), "dtype": "f16",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic_bytes(dec_traffic)},
             "cpu_baseline": cpu_dec,
         },
         "device": {"name": props.name, "cu": props.multi_processor_count,
