@@ -244,3 +244,98 @@ def test_prefill_d_head_80_f16_inputs(wrs, ctx):
                 out_layout=lq, ctx=ctx)
     ref = attention_f64(q, k, v, t_q, t_kv, H, dm)
     assert maxerr(host(out), ref) <= TOL32
+
+
+# ---- tile / step boundaries, layouts and rescale paths of the 16-bit kernel ----
+
+BOUNDARY_TKV = [31, 32, 33, 95, 96, 160, 191, 192, 193, 255, 256, 257, 320, 577]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("t_kv", BOUNDARY_TKV)
+def test_prefill_tile_boundaries(wrs, ctx, dtype, t_kv):
+    # 1..10 key tiles, partial last steps, and three query workgroups (t_q 600)
+    from wrs_amd import workloads as W
+    H, t_q = 2, 600
+    dm = H * 64
+    note(f"device prefill {dtype} t_q={t_q} t_kv={t_kv}")
+    q = W.normal((t_q, dm), 41, storage=dtype)
+    k = W.normal((t_kv, dm), 42, storage=dtype)
+    v = W.normal((t_kv, dm), 43, storage=dtype)
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    out = torch.full((t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+    wrs.prefill(dev(q, tdt), dev(k, tdt), dev(v, tdt), out, batch=1, n_heads=H, t_q=t_q,
+                t_kv=t_kv, d_head=64, q_layout=lq, kv_layout=lk, out_layout=lq, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, H, dm)
+    assert maxerr(host(out), ref) <= TOL16
+
+
+@pytest.mark.parametrize("t_q,t_kv,offset", [(600, 600, 0), (513, 700, 187), (260, 1500, 1240),
+                                             (300, 64, 0), (257, 257, 0)])
+def test_prefill_causal_workgroups(wrs, ctx, t_q, t_kv, offset):
+    # causal masks across several query workgroups, first tiles masked or not
+    from wrs_amd import workloads as W
+    H = 2
+    dm = H * 64
+    note(f"device prefill bf16 causal t_q={t_q} t_kv={t_kv} offset={offset}")
+    q = W.normal((t_q, dm), 51, storage="bf16")
+    k = W.normal((t_kv, dm), 52, storage="bf16")
+    v = W.normal((t_kv, dm), 53, storage="bf16")
+    out = torch.full((t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+    wrs.prefill(dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16), out,
+                batch=1, n_heads=H, t_q=t_q, t_kv=t_kv, d_head=64, q_layout=lq, kv_layout=lk,
+                out_layout=lq, causal=True, q_pos_offset=offset, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, H, dm, causal=True, q_offset=offset)
+    assert maxerr(host(out), ref) <= TOL16
+
+
+def test_prefill_bhsd_layout(wrs, ctx):
+    # [batch][head][token][64] tensors: row stride 64, head stride T*64
+    from wrs_amd import workloads as W
+    B, H, T = 2, 3, 333
+    note("device prefill f16 BHSD layout")
+    x = [W.normal((B, H, T, 64), 60 + i, storage="f16") for i in range(3)]
+    lay = wrs.Layout(H * T * 64, T * 64, 64)
+    out = torch.full((B, H, T, 64), float("nan"), dtype=torch.float32, device="cuda")
+    wrs.prefill(dev(x[0], torch.float16), dev(x[1], torch.float16), dev(x[2], torch.float16),
+                out, batch=B, n_heads=H, t_q=T, t_kv=T, d_head=64, q_layout=lay, kv_layout=lay,
+                out_layout=lay, ctx=ctx)
+    got = host(out)
+    for b in range(B):
+        for h in range(H):
+            ref = attention_f64(x[0][b, h], x[1][b, h], x[2][b, h], T, T, 1, 64)
+            assert maxerr(got[b, h], ref) <= TOL16, f"batch {b} head {h}"
+
+
+@pytest.mark.parametrize("profile", ["ramp", "spike"])
+def test_prefill_rescale_paths(wrs, ctx, profile):
+    # Scores whose row max keeps jumping along the keys (ramp), or one late key
+    # far above the rest (spike, weights that overflow f16 before the
+    # reference max moves): the lazy rescale must still give the exact
+    # softmax up to rounding.
+    from wrs_amd import workloads as W
+    H, t_q, t_kv = 2, 300, 900
+    dm = H * 64
+    note(f"device prefill f16 rescale profile={profile}")
+    q = W.normal((t_q, dm), 71, storage="f32")
+    k = W.normal((t_kv, dm), 72, storage="f32")
+    v = W.normal((t_kv, dm), 73, storage="f16")
+    q = np.abs(q)  # positive queries: the score grows with a positive key scale
+    if profile == "ramp":
+        k = np.abs(k) * np.linspace(0.05, 6.0, t_kv, dtype=np.float32)[:, None]
+    else:
+        k = k * 0.05
+        k[777] = 3.0
+    q = q.astype(np.float16).astype(np.float32)
+    k = k.astype(np.float16).astype(np.float32)
+    out = torch.full((t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+    wrs.prefill(dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16), out,
+                batch=1, n_heads=H, t_q=t_q, t_kv=t_kv, d_head=64, q_layout=lq, kv_layout=lk,
+                out_layout=lq, ctx=ctx)
+    got = host(out)
+    assert np.all(np.isfinite(got))
+    ref = attention_f64(q, k, v, t_q, t_kv, H, dm)
+    assert maxerr(got, ref) <= TOL16

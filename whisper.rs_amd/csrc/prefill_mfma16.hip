@@ -9,58 +9,71 @@
 // with the rounded weights.
 //
 // Work decomposition: one workgroup = 4 waves = 256 queries of one
-// (window, head); each wave owns two 32-query blocks. Per 64-key tile:
-//   S^T[64 keys x 64 q] = K_tile[64 x 64] . Q^T      (4 x 4 MFMA 32x32x16)
-//   O^T[64 d x 64 q]   += V_tile^T[64 x 64] . P^T    (4 x 4 MFMA 32x32x16 f16)
-// Every K and V^T operand read from LDS feeds the MFMAs of both query blocks,
-// which halves LDS read traffic per FLOP against one block per wave.
-// Computing S^T (keys on the MFMA M axis) puts one query per lane, so the row
-// max / row sum are register reductions plus one swap with lane^32, and the
-// S^T accumulator registers are, after exp2 and packing, exactly the B operand
-// of the PV product. V stays row-major in LDS; the transposed A operand of the
-// PV product comes from ds_read_b64_tr_b16.
+// (window, head), two workgroups per CU; each wave owns two 32-query blocks.
+// Computing S^T = K Q^T (keys on the MFMA M axis) puts one query per lane, and
+// the S^T accumulator registers are, after exp2 and packing, exactly the B
+// operand of O^T += V^T P^T. Every K and V^T operand read from LDS feeds the
+// MFMAs of both query blocks. V stays row-major in LDS; the transposed A
+// operand of the PV product comes from ds_read_b64_tr_b16.
 //
-// Pipeline: K/V tiles are triple-buffered in LDS and the loop is software
-// pipelined over 32-key half tiles, so each wave always has independent MFMA
-// and VALU work: while the VALU computes the softmax weights of half h, the
-// MFMAs of the next half's S^T run, followed by the PV MFMAs of half h. Tile
-// t+2 (in registers) is written to the third buffer and the global loads of
-// tile t+3 are in flight; one barrier per 64-key tile.
+// Per 32-key step j a wave issues, as one basic block, the S^T MFMAs of step
+// j+1, the softmax weights of step j (VALU), their row sums (4x4x4 MFMA with
+// an all-ones operand, which keeps the sum off the VALU), the PV MFMAs of step
+// j-1 and the LDS operand reads for the next step. At d_head 64 the softmax
+// VALU work is the bound, so it carries nothing the matrix pipe can do.
 //
-// Softmax rescaling is lazy: a query's reference max m only moves when a half
-// tile raises the row max by more than 2^8 (in the exp2 domain), so most
-// steps skip the O and l rescale. Weights exp2(x - m) then stay below 2^8, well inside the
-// f16 range of the PV operand, and the final 1/l normalization is unchanged.
+// K/V tiles (64 keys) move from global memory straight into LDS with
+// buffer_load ... lds (no staging registers); rows past t_kv read as zero
+// through the buffer range check. Tiles are stored unpadded with the 16-byte
+// chunks of each 128-byte row XOR-swizzled, so both the K operand reads (rows
+// r..r+15, one chunk) and the transposed V reads (rows 4i..4i+3, a chunk pair)
+// are free of bank conflicts. Four tile buffers: the steps of tile t read
+// tiles t and t+1, tile t+2 lands, tile t+3 is issued; one barrier per tile.
+// For bf16 inputs each wave converts its own V rows to f16 in place once they
+// land (exact in the f16 normal range).
+//
+// Softmax rescaling is lazy: weights are formed against a reference max that
+// may lag the true row max; a rescale (move the reference to the row max,
+// scale O and l, form the weights again) happens only when some lane's
+// partial row sum of a step exceeds 2^14, which also bounds every weight
+// inside the f16 range. The first step always rescales.
 #include "wrs_internal.hpp"
+
+#include <type_traits>
 
 namespace wrs {
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr int kQB = 2;         // 32-query blocks per wave
-constexpr int kM = 128 * kQB;  // queries per workgroup
-constexpr int kN = 64;         // keys per tile
-constexpr int kThreads = 256;  // 4 waves of 64
-constexpr int kP = 72;         // LDS row pitch of the K and V tiles, in 16-bit elements
-constexpr int kTile = kN * kP;
+constexpr int kQB = 2;              // 32-query blocks per wave
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kM = 64 * kWaves;     // queries per workgroup
+constexpr int kN = 64;              // keys per tile
+constexpr int kNB = 4;              // LDS tile buffers
+constexpr int kTileH = kN * 64;     // 16-bit elements per K (or V) tile: 8 KiB
+constexpr int kRowsPerWave = kN / kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazy = 8.0f;  // rescale threshold, log2 units
+constexpr float kSumLimit = 16384.0f;  // per-lane partial row sum that forces a rescale
+constexpr float kNoMax = -1.0e30f;     // reference max before the first step
 
 template <typename T>
 struct Elem;
 
 template <>
 struct Elem<_Float16> {
+  static constexpr bool kConvertV = false;
   static __device__ inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -70,18 +83,20 @@ struct Elem<_Float16> {
 
 template <>
 struct Elem<__bf16> {
+  static constexpr bool kConvertV = true;
   static __device__ inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  // bf16 -> f16 for the PV product: widening to f32 is a shift and the f32 ->
-  // f16 rounding is exact for bf16 values inside the f16 normal range.
+  // bf16 -> f16: widening to f32 is a shift and the f32 -> f16 rounding is
+  // exact for bf16 values inside the f16 normal range.
   static __device__ inline u32x4 to_f16(u32x4 x) {
     u32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f32x2 w = {__builtin_bit_cast(float, x[i] << 16),
-                       __builtin_bit_cast(float, x[i] & 0xffff0000u)};
+      const uint32_t xi = x[i];
+      const f32x2 w = {__builtin_bit_cast(float, xi << 16),
+                       __builtin_bit_cast(float, xi & 0xffff0000u)};
       r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(w, f16x2));
     }
     return r;
@@ -106,6 +121,41 @@ __device__ inline u32x2 read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// 16-byte chunk swizzle of a 128-byte tile row: chunk c of row r is stored at
+// c ^ swz(r). Sixteen consecutive rows reading one chunk, and four rows
+// 4i..4i+3 reading an aligned chunk pair, then hit distinct banks.
+__device__ inline int swz(int r) {
+  return ((2 * (r & 3)) | ((r >> 2) & 1)) ^ (((r >> 3) & 1) << 1);
+}
+
+// 16 bytes per lane from global memory into LDS at m0 + 16 * lane, through a
+// buffer resource (out-of-range offsets read as zero). Issued as inline asm so
+// that the compiler adds no waits of its own before later LDS reads: the
+// caller orders it with explicit vmcnt waits and barriers. m0 is written here
+// and used by nothing else in this kernel.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma16(u32x4 rsrc, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ inline u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;  // raw buffer, 32-bit data format
+  return r;
+}
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
 // Logical workgroup id with an XCD-aware remap: the hardware hands linear ids
 // round-robin to the 8 XCDs, so consecutive logical ids (the query blocks of
 // one (window, head), which read the same K/V) are gathered onto one XCD and
@@ -116,19 +166,39 @@ __device__ inline int xcd_remap(int pid, int nwg) {
   return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
 }
 
+// This wave's LDS traffic is complete, then all waves meet (no vmcnt wait:
+// tile loads in flight stay in flight).
+__device__ inline void tile_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+// Wait until at most N of this wave's tile loads are in flight.
+template <int N>
+__device__ inline void wait_tiles() {
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+typedef f32x16 SBlk[kQB];
+typedef u32x4 PBlk[kQB][2];
+
 template <typename T>
 __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, int n_qblk) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[3 * kTile];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[3 * kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kNB * kTileH];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kNB * kTileH];
 
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int lid = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
   const int qblk = lid % n_qblk;
   const int bh = lid / n_qblk;
   const int h = bh % a.n_heads;
   const int b = bh / a.n_heads;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hl = lane >> 5;
 
   const T* qp = static_cast<const T*>(a.q) + b * a.lq.bs + h * a.lq.hs;
@@ -136,14 +206,12 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const T* vp = static_cast<const T*>(a.v) + b * a.lv.bs + h * a.lv.hs;
 
   // This lane's queries: column r32 of each of the wave's S^T blocks.
-  int qi[kQB], qpos[kQB];
+  const int q0 = qblk * kM + wave * 64 + r32;
   u32x4 qf[kQB][4];
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
-    qi[j] = qblk * kM + wave * 32 * kQB + 32 * j + r32;
-    qpos[j] = qi[j] + a.q_pos_offset;
-    if (qi[j] < a.t_q) {
-      const T* row = qp + static_cast<int64_t>(qi[j]) * a.lq.rs + hl * 8;
+    if (q0 + 32 * j < a.t_q) {
+      const T* row = qp + static_cast<int64_t>(q0 + 32 * j) * a.lq.rs + hl * 8;
 #pragma unroll
       for (int dk = 0; dk < 4; ++dk) qf[j][dk] = *reinterpret_cast<const u32x4*>(row + dk * 16);
     } else {
@@ -159,44 +227,81 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     kv_end = min(kv_end, last + 1);
   }
   const int n_tiles = (kv_end + kN - 1) / kN;
-  // Tiles that need no mask: every key < t_kv and, if causal, every key at or
-  // before the first query of the block.
-  int n_full = a.t_kv / kN;
-  if (a.causal) n_full = min(n_full, (qblk * kM + a.q_pos_offset + 1) / kN);
-  n_full = min(n_full, n_tiles);
+  const int nh = 2 * n_tiles;  // 32-key steps
+  // First step that needs a mask: keys past t_kv, or (causal) past the first
+  // query of the workgroup.
+  int first_masked = a.t_kv / 32;
+  if (a.causal) first_masked = min(first_masked, (qblk * kM + a.q_pos_offset + 1) / 32);
 
-  // Cooperative tile copy: thread owns 16-byte chunks (key ci/8, columns 8*(ci%8)).
-  u32x4 kreg[2], vreg[2];
-  auto load_tile = [&](int t) {
+  // Tile copy: wave w moves rows 16w..16w+15 of each K and V tile, 8 rows
+  // (1 KiB, one DMA) at a time; lane i carries row i/8, chunk i%8 of them.
+  const int crow0 = kRowsPerWave * wave + (lane >> 3);
+  const int crow1 = crow0 + 8;
+  const int cch0 = (lane & 7) ^ swz(crow0), cch1 = (lane & 7) ^ swz(crow1);
+  const uint32_t kofs0 = static_cast<uint32_t>((crow0 * a.lk.rs + cch0 * 8) * 2);
+  const uint32_t kofs1 = static_cast<uint32_t>((crow1 * a.lk.rs + cch1 * 8) * 2);
+  const uint32_t vofs0 = static_cast<uint32_t>((crow0 * a.lv.rs + cch0 * 8) * 2);
+  const uint32_t vofs1 = static_cast<uint32_t>((crow1 * a.lv.rs + cch1 * 8) * 2);
+  const uint32_t kstep = static_cast<uint32_t>(kN * a.lk.rs * 2);
+  const uint32_t vstep = static_cast<uint32_t>(kN * a.lv.rs * 2);
+  const u32x4 krs = buffer_rsrc(kp, static_cast<uint32_t>(((a.t_kv - 1) * a.lk.rs + 64) * 2));
+  const u32x4 vrs = buffer_rsrc(vp, static_cast<uint32_t>(((a.t_kv - 1) * a.lv.rs + 64) * 2));
+  const uint32_t ks_lds = lds_addr(Ks) + wave * kRowsPerWave * 128;
+  const uint32_t vs_lds = lds_addr(Vs) + wave * kRowsPerWave * 128;
+  auto issue_tile = [&](int t) {
+    const uint32_t buf = __builtin_amdgcn_readfirstlane((t % kNB) * (kTileH * 2));
+    dma16(krs, ks_lds + buf, kofs0 + t * kstep);
+    dma16(krs, ks_lds + buf + 1024, kofs1 + t * kstep);
+    dma16(vrs, vs_lds + buf, vofs0 + t * vstep);
+    dma16(vrs, vs_lds + buf + 1024, vofs1 + t * vstep);
+  };
+  // bf16 V -> f16 in place: this wave's own rows, whose loads have landed.
+  auto convert_tile = [&](int t) {
+    if constexpr (Elem<T>::kConvertV) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int ci = tid + r * kThreads;
-      const int key = t * kN + (ci >> 3), col = (ci & 7) * 8;
-      kreg[r] = vreg[r] = u32x4{0, 0, 0, 0};
-      if (key < a.t_kv) {
-        kreg[r] = *reinterpret_cast<const u32x4*>(kp + static_cast<int64_t>(key) * a.lk.rs + col);
-        vreg[r] = *reinterpret_cast<const u32x4*>(vp + static_cast<int64_t>(key) * a.lv.rs + col);
+      for (int r = 0; r < 2; ++r) {
+        u32x4* p = reinterpret_cast<u32x4*>(Vs + (t % kNB) * kTileH + wave * kRowsPerWave * 64 +
+                                            r * 512 + lane * 8);
+        *p = Elem<T>::to_f16(*p);
       }
     }
   };
-  auto store_tile = [&](int buf) {
+
+  // Per-lane LDS offsets (elements) of the MFMA operand reads. K A operand:
+  // row r32, chunks hl + 2*dk. V^T operand (transposed read): lane group
+  // g = lane/16 reads rows 4*(g/2) + (lane%16)/4 [+8] at columns
+  // 16*(g%2) + 4*(lane%4) [+32], so lane (d, hl) receives keys 4*hl + 0..3 [+8].
+  int koff[4];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int ci = tid + r * kThreads;
-      const int off = buf * kTile + (ci >> 3) * kP + (ci & 7) * 8;
-      *reinterpret_cast<u32x4*>(Ks + off) = kreg[r];
-      *reinterpret_cast<u32x4*>(Vs + off) = Elem<T>::to_f16(vreg[r]);
+  for (int dk = 0; dk < 4; ++dk) koff[dk] = r32 * 64 + (((hl + 2 * dk) ^ swz(r32)) * 8);
+  const int g = lane >> 4, t4 = lane & 15;
+  int voff[2][2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int row = 4 * (g >> 1) + (t4 >> 2) + 8 * e;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const int chunk = 2 * (g & 1) + ((t4 & 3) >> 1) + 4 * cc;
+      voff[e][cc] = row * 64 + ((chunk ^ swz(row)) * 8) + 4 * (t4 & 1);
+    }
+  }
+  auto kfetch = [&](int step, u32x4 (&ka)[4]) {
+    const uint16_t* kt = Ks + ((step >> 1) % kNB) * kTileH + (step & 1) * 32 * 64;
+#pragma unroll
+    for (int dk = 0; dk < 4; ++dk) ka[dk] = *reinterpret_cast<const u32x4*>(kt + koff[dk]);
+  };
+  auto vfetch = [&](int step, u32x2 (&va)[8]) {
+    const uint16_t* vt = Vs + ((step >> 1) % kNB) * kTileH + (step & 1) * 32 * 64;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const uint16_t* v0 = vt + 16 * k2 * 64;
+      va[4 * k2 + 0] = read_tr(v0 + voff[0][0]);
+      va[4 * k2 + 1] = read_tr(v0 + voff[1][0]);
+      va[4 * k2 + 2] = read_tr(v0 + voff[0][1]);
+      va[4 * k2 + 3] = read_tr(v0 + voff[1][1]);
     }
   };
-
-  // K A-operands of half h2 of the tile in buffer buf, and S^T = K Q^T for
-  // those 32 keys and both query blocks.
-  typedef f32x16 SBlk[kQB];
-  auto kfetch = [&](int buf, int h2, u32x4 (&ka)[4]) {
-    const uint16_t* kt = Ks + buf * kTile + (32 * h2 + r32) * kP + hl * 8;
-#pragma unroll
-    for (int dk = 0; dk < 4; ++dk) ka[dk] = *reinterpret_cast<const u32x4*>(kt + dk * 16);
-  };
+  // S^T = K Q^T for 32 keys and both query blocks.
   auto qk = [&](const u32x4 (&ka)[4], SBlk& s) {
 #pragma unroll
     for (int j = 0; j < kQB; ++j) s[j] = f32x16{};
@@ -206,84 +311,65 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       for (int j = 0; j < kQB; ++j) s[j] = Elem<T>::mfma(ka[dk], qf[j][dk], s[j]);
   };
 
-  const float c = a.scale * kLog2e;  // exp(scale*s - m') == exp2(c*s - c*m)
+  const float c = a.scale * kLog2e;  // exp(scale*s - m') == exp2(c*s - m)
   f32x16 o[kQB][2];                  // O^T rows d 0..31 / 32..63, column = query
   float m[kQB], l[kQB];              // reference max (exp2 domain), partial row sum
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
     o[j][0] = o[j][1] = f32x16{};
-    m[j] = -INFINITY;
+    m[j] = kNoMax;
     l[j] = 0.f;
   }
 
   // Accumulator register i of a 32x32 block holds key 8*(i/4) + 4*hl + i%4 of
-  // its 32-key half.
-  auto mask_half = [&](int t, int h2, SBlk& s) {
+  // its 32-key step.
+  auto mask_step = [&](int step, SBlk& s) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int kr = t * kN + 32 * h2 + 8 * (i >> 2) + 4 * hl + (i & 3);
+      const int kr = 32 * step + 8 * (i >> 2) + 4 * hl + (i & 3);
 #pragma unroll
-      for (int j = 0; j < kQB; ++j)
-        if (kr >= a.t_kv || (a.causal && kr > qpos[j])) s[j][i] = -INFINITY;
-    }
-  };
-  // Row max of a half tile in the exp2 domain; if it exceeds the reference max
-  // by more than kLazy, move the reference and rescale what is accumulated.
-  auto rescale_for = [&](const SBlk& s) {
-#pragma unroll
-    for (int j = 0; j < kQB; ++j) {
-      float mr = fmaxf(s[j][0], s[j][1]);
-#pragma unroll
-      for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s[j][i]), s[j][i + 1]);  // v_max3
-      const float mx = pair_max(mr) * c;
-      if (mx > m[j] + kLazy) {
-        const float alpha = __builtin_amdgcn_exp2f(m[j] - mx);  // m == -inf -> 0
-        m[j] = mx;
-        l[j] *= alpha;
-        o[j][0] *= alpha;
-        o[j][1] *= alpha;
+      for (int j = 0; j < kQB; ++j) {
+        const int qpos = q0 + 32 * j + a.q_pos_offset;
+        s[j][i] = ((kr >= a.t_kv) | ((a.causal != 0) & (kr > qpos))) ? -INFINITY : s[j][i];
       }
     }
   };
-  // P = exp2(c*S - m) in f16 and O^T += V^T P^T.
-  // P^T is already in B-operand order: PV block kb2 covers tile keys
-  // 16*kb2 + 8*(j/4) + 4*hl + j%4 for element j. V^T rows come from the
-  // transposed read: lane group g = lane/16 reads rows 16*kb2 + 4*(g/2) [+8]
-  // + (lane%16)/4 at columns 32*db + 16*(g%2) + 4*(lane%4), so lane
-  // (d = 32*db + r32, hl) receives keys 16*kb2 + 4*hl + {0..3} [+8].
-  const int g = lane >> 4, t4 = lane & 15;
-  const int vlane = (4 * (g >> 1) + (t4 >> 2)) * kP + 16 * (g & 1) + 4 * (t4 & 3);
-  auto vfetch = [&](int buf, int h2, u32x2 (&va)[8]) {
-    const uint16_t* vrow = Vs + buf * kTile + vlane + 32 * h2 * kP;
+  // P = exp2(c*S - m) as packed f16 pairs, already in B-operand order for the
+  // PV product: block k2 covers step keys 16*k2 + 8*(w/2) + 4*hl + {0..3}.
+  auto weights = [&](const SBlk& s, PBlk& pb) {
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      const uint16_t* v0 = vrow + 16 * k2 * kP;
-      va[4 * k2 + 0] = read_tr(v0);
-      va[4 * k2 + 1] = read_tr(v0 + 8 * kP);
-      va[4 * k2 + 2] = read_tr(v0 + 32);
-      va[4 * k2 + 3] = read_tr(v0 + 8 * kP + 32);
-    }
-  };
-  auto weights = [&](const SBlk& s, u32x4 (&pb)[kQB][2]) {
+    for (int j = 0; j < kQB; ++j)
 #pragma unroll
-    for (int j = 0; j < kQB; ++j) {
-      float ls = 0.f;
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
+      for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const f32x2 pp = {
               __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][8 * k2 + 2 * w], c, -m[j])),
               __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][8 * k2 + 2 * w + 1], c, -m[j]))};
-          const f16x2 hp = __builtin_convertvector(pp, f16x2);
-          ls = __builtin_amdgcn_fdot2(hp, f16x2{1.0f16, 1.0f16}, ls, false);
-          pb[j][k2][w] = __builtin_bit_cast(uint32_t, hp);
+          pb[j][k2][w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pp, f16x2));
         }
-      }
-      l[j] += ls;
+  };
+  // Per-lane sum of the 16 rounded weights of each query block on the matrix
+  // pipe: a 4x4x4 (16-block) MFMA with an all-ones A operand returns, in every
+  // register of a lane, the f32 sum of the lane's four f16 B values.
+  const f16x4 ones = {1.0f16, 1.0f16, 1.0f16, 1.0f16};
+  auto row_sums = [&](const PBlk& pb, f32x4 (&ls)[kQB]) {
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int w = 0; w < 4; w += 2) {
+          const uint32_t lo = pb[j][k2][w], hi = pb[j][k2][w + 1];
+          acc = __builtin_amdgcn_mfma_f32_4x4x4f16(ones, __builtin_bit_cast(f16x4, u32x2{lo, hi}),
+                                                   acc, 0, 0, 0);
+        }
+      ls[j] = acc;
     }
   };
-  auto pv = [&](const u32x2 (&va)[8], const u32x4 (&pb)[kQB][2]) {
+  // O^T += V^T P^T for one 32-key step.
+  auto pv = [&](const u32x2 (&va)[8], const PBlk& pb) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       const u32x4 v0 = {va[4 * k2].x, va[4 * k2].y, va[4 * k2 + 1].x, va[4 * k2 + 1].y};
@@ -295,81 +381,124 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       }
     }
   };
-  // One half step, in issue order: S^T MFMAs of the next half (K operands
-  // already in registers), V^T reads and softmax weights of this half (the
-  // VALU work overlaps those MFMAs), PV MFMAs of this half, K operands two
-  // halves ahead. The caller then reduces the next half's row max (its MFMAs
-  // have long finished) while the PV MFMAs drain.
-  auto half_step = [&](int buf, int h2, const SBlk& s, u32x4 (&ka)[4], int kbuf, int kh2,
-                       bool fetch_k, SBlk& n) {
-    qk(ka, n);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x2 va[8];
-    vfetch(buf, h2, va);
-    u32x4 pb[kQB][2];
-    weights(s, pb);
-    __builtin_amdgcn_sched_barrier(0);
-    pv(va, pb);
-    if (fetch_k) kfetch(kbuf, kh2, ka);
-    __builtin_amdgcn_sched_barrier(0);
+  // Lazy rescale (see the file header): after a step's weights are formed,
+  // move the reference max when some lane's partial row sum is out of range
+  // (always on the first step), rescale O and l, and form the weights again;
+  // then fold the step's row sums into l.
+  auto settle = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
+    bool need = false;
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) need |= !(ls[j][0] <= kSumLimit);
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int j = 0; j < kQB; ++j) {
+        float mr = fmaxf(s[j][0], s[j][1]);
+#pragma unroll
+        for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s[j][i]), s[j][i + 1]);  // v_max3
+        const float mx = pair_max(mr) * c;
+        if (mx > m[j]) {
+          const float alpha = __builtin_amdgcn_exp2f(m[j] - mx);
+          m[j] = mx;
+          l[j] *= alpha;
+          o[j][0] *= alpha;
+          o[j][1] *= alpha;
+        }
+      }
+      weights(s, pb);
+      row_sums(pb, ls);
+    }
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) l[j] += ls[j][0];
   };
 
   if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-    if (n_tiles > 1) {
-      load_tile(1);
-      store_tile(1);
-      if (n_tiles > 2) load_tile(2);
-    }
-    __syncthreads();
+    issue_tile(0);
+    if (n_tiles > 1) issue_tile(1);
+    if (n_tiles > 2) issue_tile(2);
+    wait_tiles<0>();
+    convert_tile(0);
+    if (n_tiles > 1) convert_tile(1);
+    if (n_tiles > 2) convert_tile(2);
+    tile_barrier();
+
+    SBlk sa, sb;
+    PBlk pa, pbb;
     u32x4 ka[4];
-    kfetch(0, 0, ka);
-    SBlk s, n;
-    qk(ka, s);
-    if (n_full == 0) mask_half(0, 0, s);
-    rescale_for(s);
-    kfetch(0, 1, ka);
-    int t = 0;
-    // Main loop: tiles t and t+1 both unmasked (and t+1 already in LDS).
-    for (; t + 1 < n_full; ++t) {
-      if (t + 2 < n_tiles) {
-        store_tile((t + 2) % 3);
-        if (t + 3 < n_tiles) load_tile(t + 3);
+    u32x2 va[8];
+    f32x4 ls[kQB];
+    kfetch(0, ka);
+    qk(ka, sa);
+    kfetch(1, ka);
+
+    // Step j: S of step j+1, weights and row sums of step j, PV of step j-1,
+    // then the operand reads for the next step (K of step j+2, V of step j),
+    // then the lazy-rescale check of step j. Full steps have every part and
+    // no mask, so their body is one basic block, interleaved as groups of one
+    // MFMA and a few VALU instructions.
+    auto step = [&](auto full_tag, int j, SBlk& s_in, SBlk& s_out, PBlk& p_out,
+                    PBlk& p_in) __attribute__((always_inline)) {
+      constexpr bool kFull = decltype(full_tag)::value;
+      if (kFull || j + 1 < nh) qk(ka, s_out);
+      if (!kFull && j >= first_masked) mask_step(j, s_in);
+      weights(s_in, p_out);
+      row_sums(p_out, ls);
+      if (kFull || j >= 1) pv(va, p_in);
+      if (kFull || j + 2 < nh) kfetch(j + 2, ka);
+      vfetch(j, va);
+      if constexpr (kFull) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);    // DS read
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
       }
-      const int buf = t % 3, nbuf = (t + 1) % 3;
-      half_step(buf, 0, s, ka, nbuf, 0, true, n);  // S of (t, 1); K of (t+1, 0)
-      rescale_for(n);
-      half_step(buf, 1, n, ka, nbuf, 1, true, s);  // S of (t+1, 0); K of (t+1, 1)
-      rescale_for(s);
-      __syncthreads();
-    }
-    // Tail: the last unmasked tile and the masked ones.
-    for (; t < n_tiles; ++t) {
-      if (t + 2 < n_tiles) {
-        store_tile((t + 2) % 3);
-        if (t + 3 < n_tiles) load_tile(t + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      settle(s_in, p_out, ls);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    typedef std::integral_constant<bool, true> Full;
+    typedef std::integral_constant<bool, false> Part;
+
+    // Tile t covers steps 2t and 2t+1, which read tiles t and t+1. Tile t+3
+    // is issued into the buffer of tile t-1 (free since the last barrier);
+    // tile t+2 lands and is converted before the barrier that ends tile t.
+    auto tile = [&](auto full_tag, int t) __attribute__((always_inline)) {
+      const bool more = t + 3 < n_tiles;
+      if (more) issue_tile(t + 3);
+      step(full_tag, 2 * t, sa, sb, pa, pbb);
+      step(full_tag, 2 * t + 1, sb, sa, pbb, pa);
+      if (t + 2 < n_tiles && t > 0) {
+        if (more)
+          wait_tiles<4>();
+        else
+          wait_tiles<0>();
+        convert_tile(t + 2);
       }
-      const int buf = t % 3, nbuf = (t + 1) % 3;
-      const bool has_next = t + 1 < n_tiles;
-      half_step(buf, 0, s, ka, nbuf, 0, has_next, n);
-      if (t >= n_full) mask_half(t, 1, n);
-      rescale_for(n);
-      half_step(buf, 1, n, ka, nbuf, 1, has_next, s);
-      if (has_next) {
-        if (t + 1 >= n_full) mask_half(t + 1, 0, s);
-        rescale_for(s);
-      }
-      __syncthreads();
-    }
+      tile_barrier();
+    };
+    // Tile 0 (no PV yet), full tiles (both steps complete and unmasked), then
+    // the tail.
+    const int t_full_end = min(n_tiles - 1, first_masked / 2);
+    tile(Part{}, 0);
+    int t = 1;
+    for (; t < t_full_end; ++t) tile(Full{}, t);
+    for (; t < n_tiles; ++t) tile(Part{}, t);
+    pv(va, pbb);  // last step (odd): weights in pbb
   }
 
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
     l[j] = pair_sum(l[j]);
     const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
-    if (qi[j] < a.t_q) {
-      float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(qi[j]) * a.lo.rs;
+    if (q0 + 32 * j < a.t_q) {
+      float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(q0 + 32 * j) * a.lo.rs;
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         *reinterpret_cast<f32x4*>(op + 8 * gq + 4 * hl) =
@@ -385,7 +514,17 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
 
 }  // namespace
 
+bool prefill_mfma16_supports(const PrefillArgs& a) {
+  // K/V rows are addressed through 32-bit buffer offsets, and the range check
+  // that zero-fills keys past t_kv needs rows at least one head wide.
+  const int64_t span_k = (static_cast<int64_t>(a.t_kv) + kN) * a.lk.rs * 2;
+  const int64_t span_v = (static_cast<int64_t>(a.t_kv) + kN) * a.lv.rs * 2;
+  return a.d_head == 64 && a.lk.rs >= 64 && a.lv.rs >= 64 && span_k < (int64_t{1} << 31) &&
+         span_v < (int64_t{1} << 31);
+}
+
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) {
+  if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
   const int n_qblk = (a.t_q + kM - 1) / kM;
   const int64_t nwg = static_cast<int64_t>(n_qblk) * a.n_heads * a.batch;
   if (nwg <= 0) return hipSuccess;

@@ -204,7 +204,7 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
            l.head_stride % mult == 0 && l.row_stride % mult == 0;
   };
   if (same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
-      aligned16(v, lv, 8) && aligned16(out, lo, 4)) {
+      aligned16(v, lv, 8) && aligned16(out, lo, 4) && wrs::prefill_mfma16_supports(a)) {
     WRS_HIP(c, wrs::launch_prefill_mfma16(a, q_dtype == WRS_F16 ? wrs::kF16 : wrs::kBF16,
                                           c->stream));
     return WRS_OK;

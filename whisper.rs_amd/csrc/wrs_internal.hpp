@@ -35,7 +35,9 @@ struct PrefillArgs {
   float scale;       // 1/sqrt(d_head), rounded to f32 like attention.rs:107
 };
 
-// MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type.
+// MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type, rows 16-byte
+// aligned; prefill_mfma16_supports() states the remaining shape limits.
+bool prefill_mfma16_supports(const PrefillArgs& a);
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s);
 // f32-accumulate-check kernel on f32 MFMA: q f32, k/v f32|f16|bf16 widened
 // exactly to f32, any d_head <= 128.
