@@ -251,8 +251,9 @@ def cpu_baseline_decode(cfg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    # ~75 ms of untimed encoder steps: the clocks settle within about 300 steps
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--decode-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--eager", action="store_true",
