@@ -191,6 +191,27 @@ def test_cross_decode_beam_counts(wrs, ctx, beams):
     arena.close()
 
 
+@pytest.mark.parametrize("n_audio", [129, 1536, 1537, 2900])
+def test_cross_decode_split_counts(wrs, ctx, n_audio):
+    # 128 keys per split: 2, 12 (largest one-round merge), 13 and 23 splits
+    # (batched merge) per (beam group, head).
+    from wrs_amd import workloads as W
+    H, dm, beams = 4, 256, 5
+    note(f"device decode_cross n_audio={n_audio}")
+    arena = wrs.KvArena(1, 1, H, 448, 3000, ctx=ctx)
+    k = W.normal((n_audio, dm), 90, storage="f16")
+    v = W.normal((n_audio, dm), 91, storage="f16")
+    arena.set_cross(0, k, v)
+    q = W.normal((beams, dm), 92)
+    out = torch.full((beams, dm), float("nan"), device="cuda")
+    for _ in range(2):  # the second launch reuses the re-armed counters
+        arena.decode_cross(0, dev(q), out)
+        got = host(out)
+        ref = attention_f64(q, k, v, beams, n_audio, H, dm)
+        assert maxerr(got, ref) <= TOL16
+    arena.close()
+
+
 # ---- prompt rows over the arena ------------------------------------------------
 
 def test_prefill_self_prompt_rows(wrs, orc, ctx):

@@ -14,8 +14,8 @@
 //   thread bumps the (group, head) counter -- each on its own 128-byte line, so
 //   the increments of different heads do not serialize. The workgroup that
 //   sees the last count merges all splits with the log-sum-exp rule, reading
-//   the partials with agent-scope loads issued 16 at a time, writes the output
-//   and re-arms its counter. Agent-scope atomics avoid the full-L2 writeback
+//   the partials with agent-scope loads (all splits at once up to 12 splits,
+//   else 16 at a time), writes the output and re-arms its counter. Agent-scope atomics avoid the full-L2 writeback
 //   and invalidate that a device-wide __threadfence costs on gfx950.
 //
 // decode_exact_f32: the reference's own decode arithmetic on f32 K/V for the
@@ -35,7 +35,8 @@ constexpr int kChunk = kDecodeChunk;  // keys per workgroup: 2 per thread, 4 thr
 constexpr int kKpt = kChunk / 64;
 constexpr int kPart = 68;    // floats per partial row: m, l, 2 pad, acc[64]
 constexpr int kCounterStride = 32;  // 128 bytes between merge counters
-constexpr int kMergeBatch = 16;     // partial loads in flight per thread
+constexpr int kMergeBatch = 16;     // partial loads in flight per thread (long rows)
+constexpr int kMaxSplitsMerge = 12; // splits merged in one round (rows up to 1536 keys)
 
 // Cross-lane moves inside a row of 16 lanes (DPP): xor 1, xor 2, mirror-8, mirror-16.
 template <int CTRL>
@@ -218,41 +219,91 @@ __global__ __launch_bounds__(kThreads) void decode_f16(DecodeArgs a) {
   __syncthreads();
   if (!last_flag) return;
 
-  // Log-sum-exp merge of all splits (exp2 domain), batches of kMergeBatch
-  // splits with their loads issued together, folded online across batches.
+  // Log-sum-exp merge of all splits (exp2 domain).
   const float* base = a.part + static_cast<int64_t>(gh) * a.n_splits * rows * kPart;
-  for (int e = tid; e < rows * 64; e += kThreads) {
-    const int r = e >> 6, d = e & 63;
-    float M = -INFINITY, L = 0.f, acc = 0.f;
-    for (int s0 = 0; s0 < a.n_splits; s0 += kMergeBatch) {
-      float ms[kMergeBatch], ls[kMergeBatch], as[kMergeBatch];
+  const int ns = a.n_splits;
+  if (ns <= kMaxSplitsMerge) {
+    // One round: a thread merges two (row, d) elements and issues the partial
+    // loads of both, for every split, before any arithmetic.
+    for (int e0 = tid; e0 < rows * 64; e0 += 2 * kThreads) {
+      const int e1 = e0 + kThreads;
+      const bool two = e1 < rows * 64;
+      const int r0 = e0 >> 6, r1 = two ? (e1 >> 6) : r0, d0 = e0 & 63, d1 = e1 & 63;
+      float m0[kMaxSplitsMerge], l0[kMaxSplitsMerge], x0[kMaxSplitsMerge];
+      float m1[kMaxSplitsMerge], l1[kMaxSplitsMerge], x1[kMaxSplitsMerge];
 #pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) {
-        ms[j] = -INFINITY;
-        ls[j] = as[j] = 0.f;
-        if (s0 + j < a.n_splits) {
-          const float* pr = base + ((s0 + j) * rows + r) * kPart;
-          ms[j] = ld_agent(pr);
-          ls[j] = ld_agent(pr + 1);
-          as[j] = ld_agent(pr + 4 + d);
+      for (int sp = 0; sp < kMaxSplitsMerge; ++sp) {
+        m0[sp] = m1[sp] = -INFINITY;
+        l0[sp] = l1[sp] = x0[sp] = x1[sp] = 0.f;
+        if (sp < ns) {
+          const float* p0 = base + (sp * rows + r0) * kPart;
+          m0[sp] = ld_agent(p0);
+          l0[sp] = ld_agent(p0 + 1);
+          x0[sp] = ld_agent(p0 + 4 + d0);
+          if (two) {
+            const float* p1 = base + (sp * rows + r1) * kPart;
+            m1[sp] = ld_agent(p1);
+            l1[sp] = ld_agent(p1 + 1);
+            x1[sp] = ld_agent(p1 + 4 + d1);
+          }
         }
       }
-      float Mb = M;
+      float M0 = -INFINITY, M1 = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, ms[j]);
-      if (Mb == -INFINITY) continue;
-      const float scale = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mb);
-      L *= scale;
-      acc *= scale;
-#pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) {
-        const float w = (ms[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[j] - Mb);
-        L = __builtin_fmaf(ls[j], w, L);
-        acc = __builtin_fmaf(as[j], w, acc);
+      for (int sp = 0; sp < kMaxSplitsMerge; ++sp) {
+        M0 = fmaxf(M0, m0[sp]);
+        M1 = fmaxf(M1, m1[sp]);
       }
-      M = Mb;
+      float L0 = 0.f, A0 = 0.f, L1 = 0.f, A1 = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplitsMerge; ++sp) {
+        const float w0 = (m0[sp] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m0[sp] - M0);
+        const float w1 = (m1[sp] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m1[sp] - M1);
+        L0 = __builtin_fmaf(l0[sp], w0, L0);
+        A0 = __builtin_fmaf(x0[sp], w0, A0);
+        L1 = __builtin_fmaf(l1[sp], w1, L1);
+        A1 = __builtin_fmaf(x1[sp], w1, A1);
+      }
+      a.o[static_cast<int64_t>(g * rows + r0) * a.o_rs + h * 64 + d0] = L0 > 0.f ? A0 * (1.f / L0) : 0.f;
+      if (two)
+        a.o[static_cast<int64_t>(g * rows + r1) * a.o_rs + h * 64 + d1] = L1 > 0.f ? A1 * (1.f / L1) : 0.f;
     }
-    a.o[static_cast<int64_t>(g * rows + r) * a.o_rs + h * 64 + d] = L > 0.f ? acc * (1.f / L) : 0.f;
+  } else {
+    // Longer rows: batches of kMergeBatch splits with their loads issued
+    // together, folded online across batches.
+    for (int e = tid; e < rows * 64; e += kThreads) {
+      const int r = e >> 6, d = e & 63;
+      float M = -INFINITY, L = 0.f, acc = 0.f;
+      for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+        float ms[kMergeBatch], ls[kMergeBatch], as[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+          ms[j] = -INFINITY;
+          ls[j] = as[j] = 0.f;
+          if (s0 + j < ns) {
+            const float* pr = base + ((s0 + j) * rows + r) * kPart;
+            ms[j] = ld_agent(pr);
+            ls[j] = ld_agent(pr + 1);
+            as[j] = ld_agent(pr + 4 + d);
+          }
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, ms[j]);
+        if (Mb == -INFINITY) continue;
+        const float scale = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mb);
+        L *= scale;
+        acc *= scale;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+          const float w = (ms[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[j] - Mb);
+          L = __builtin_fmaf(ls[j], w, L);
+          acc = __builtin_fmaf(as[j], w, acc);
+        }
+        M = Mb;
+      }
+      a.o[static_cast<int64_t>(g * rows + r) * a.o_rs + h * 64 + d] = L > 0.f ? acc * (1.f / L) : 0.f;
+    }
   }
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
