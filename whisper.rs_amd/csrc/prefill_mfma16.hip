@@ -17,10 +17,11 @@
 // operand of the PV product comes from ds_read_b64_tr_b16.
 //
 // Per 32-key step j a wave issues, as one basic block, the S^T MFMAs of step
-// j+1, the softmax weights of step j (VALU), their row sums (4x4x4 MFMA with
-// an all-ones operand, which keeps the sum off the VALU), the PV MFMAs of step
-// j-1 and the LDS operand reads for the next step. At d_head 64 the softmax
-// VALU work is the bound, so it carries nothing the matrix pipe can do.
+// j+1 and the PV MFMAs of step j-1 interleaved with the softmax weights of
+// step j (VALU), then the row sums of step j (16x16x32 MFMAs with a 0/1
+// selector operand, which keeps the sum off the VALU) and the LDS operand
+// reads for the next step. At d_head 64 the softmax VALU work is the bound,
+// so it carries nothing the matrix pipe can do.
 //
 // K/V tiles (64 keys) move from global memory straight into LDS with
 // buffer_load ... lds (no staging registers); rows past t_kv read as zero
@@ -34,9 +35,9 @@
 //
 // Softmax rescaling is lazy: weights are formed against a reference max that
 // may lag the true row max; a rescale (move the reference to the row max,
-// scale O and l, form the weights again) happens only when some lane's
-// partial row sum of a step exceeds 2^14, which also bounds every weight
-// inside the f16 range. The first step always rescales.
+// scale O and l, form the weights again) happens only when some query's row
+// sum over a step exceeds 2^14, which also bounds every weight inside the f16
+// range. The first step always rescales.
 #include "wrs_internal.hpp"
 
 #include <type_traits>
@@ -65,7 +66,7 @@ constexpr int kNB = 4;              // LDS tile buffers
 constexpr int kTileH = kN * 64;     // 16-bit elements per K (or V) tile: 8 KiB
 constexpr int kRowsPerWave = kN / kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kSumLimit = 16384.0f;  // per-lane partial row sum that forces a rescale
+constexpr float kSumLimit = 16384.0f;  // row sum of one step that forces a rescale
 constexpr float kNoMax = -1.0e30f;     // reference max before the first step
 
 template <typename T>
@@ -112,7 +113,6 @@ __device__ inline f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
 // (ds_bpermute via __shfl_xor: this toolchain miscompiles
 // __builtin_amdgcn_permlane32_swap when both operands are the same value.)
 __device__ inline float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
-__device__ inline float pair_sum(float x) { return x + __shfl_xor(x, 32); }
 
 // Four consecutive keys of one d column, from a row-major [key][d] LDS tile.
 __device__ inline u32x2 read_tr(const uint16_t* p) {
@@ -349,23 +349,23 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
           pb[j][k2][w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pp, f16x2));
         }
   };
-  // Per-lane sum of the 16 rounded weights of each query block on the matrix
-  // pipe: a 4x4x4 (16-block) MFMA with an all-ones A operand returns, in every
-  // register of a lane, the f32 sum of the lane's four f16 B values.
-  const f16x4 ones = {1.0f16, 1.0f16, 1.0f16, 1.0f16};
+  // Row sums of the rounded weights on the matrix pipe. Read as the B operand
+  // of a 16x16x32 MFMA, the weight registers of 16 keys put the keys of query
+  // n (lanes n and n+32, n < 32) in column n mod 16, k-groups n/16 and n/16+2.
+  // A selector A operand that is 1 exactly where (row/4) and the k-group have
+  // the same parity leaves, in every register of lane l, the f32 sum of the
+  // 16 weights of query l mod 32. Rows of the other query in the column meet
+  // zeros, so an infinite weight there turns this sum into NaN; the rescale
+  // check below treats NaN like an overflow.
+  const _Float16 rs_one = ((lane >> 2) & 1) == ((lane >> 4) & 1) ? 1.0f16 : 0.0f16;
+  const f16x8 rs_sel = {rs_one, rs_one, rs_one, rs_one, rs_one, rs_one, rs_one, rs_one};
   auto row_sums = [&](const PBlk& pb, f32x4 (&ls)[kQB]) {
 #pragma unroll
     for (int j = 0; j < kQB; ++j) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-        for (int w = 0; w < 4; w += 2) {
-          const uint32_t lo = pb[j][k2][w], hi = pb[j][k2][w + 1];
-          acc = __builtin_amdgcn_mfma_f32_4x4x4f16(ones, __builtin_bit_cast(f16x4, u32x2{lo, hi}),
-                                                   acc, 0, 0, 0);
-        }
-      ls[j] = acc;
+      const f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          rs_sel, __builtin_bit_cast(f16x8, pb[j][0]), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      ls[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(rs_sel, __builtin_bit_cast(f16x8, pb[j][1]),
+                                                     acc, 0, 0, 0);
     }
   };
   // O^T += V^T P^T for one 32-key step.
@@ -388,7 +388,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   auto settle = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
     bool need = false;
 #pragma unroll
-    for (int j = 0; j < kQB; ++j) need |= !(ls[j][0] <= kSumLimit);
+    // Unsigned compare of the bit patterns: true for sums above the limit,
+    // inf and NaN alike (the kernel is built without NaN semantics, so a
+    // float compare may not see NaN). Row sums are never negative.
+    for (int j = 0; j < kQB; ++j)
+      need |= __builtin_bit_cast(uint32_t, ls[j][0]) > __builtin_bit_cast(uint32_t, kSumLimit);
     if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
       for (int j = 0; j < kQB; ++j) {
@@ -446,18 +450,25 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       if (kFull || j + 2 < nh) kfetch(j + 2, ka);
       vfetch(j, va);
       if constexpr (kFull) {
+        // 16 S/PV MFMAs spread over the softmax, then the 4 row-sum MFMAs
+        // (they need the last weights), with the LDS reads in between.
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);    // DS read
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 8; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       settle(s_in, p_out, ls);
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
 
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
-    l[j] = pair_sum(l[j]);
+    // l is the whole row sum in both lanes of the query (the row sums are).
     const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
     if (q0 + 32 * j < a.t_q) {
       float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(q0 + 32 * j) * a.lo.rs;
