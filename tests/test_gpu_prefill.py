@@ -163,6 +163,36 @@ def test_large_encoder_bf16(wrs, orc, ctx):
     assert np.array_equal(alone[0], out[7])
 
 
+@pytest.mark.parametrize("t", [1000, 1500])
+def test_prefill_many_query_blocks(wrs, ctx, t):
+    # Several rounds of workgroups (640 query blocks): every window of the
+    # batch equals the same window run alone, bitwise, and matches the
+    # float64 reference.
+    from wrs_amd import workloads as W
+    B, H = 40, 4
+    dm = H * 64
+    note(f"device prefill f16 many blocks: batch {B} heads {H} t {t}")
+    q = W.normal((B, t, dm), 80, storage="f16")
+    k = W.normal((B, t, dm), 81, storage="f16")
+    v = W.normal((B, t, dm), 82, storage="f16")
+    k[:, ::7] *= 2.0  # spread the row maxima over the key range (exact in f16)
+    lay = wrs.token_major(t, dm, 64)
+    qd, kd, vd = dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16)
+    out = torch.full((B, t, dm), float("nan"), dtype=torch.float32, device="cuda")
+    wrs.prefill(qd, kd, vd, out, batch=B, n_heads=H, t_q=t, t_kv=t, d_head=64, q_layout=lay,
+                kv_layout=lay, out_layout=lay, ctx=ctx)
+    got = host(out)
+    assert np.all(np.isfinite(got))
+    one = torch.full((1, t, dm), float("nan"), dtype=torch.float32, device="cuda")
+    for b in range(B):
+        wrs.prefill(qd[b:b + 1], kd[b:b + 1], vd[b:b + 1], one, batch=1, n_heads=H, t_q=t,
+                    t_kv=t, d_head=64, q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+        assert np.array_equal(got[b], host(one)[0]), f"window {b}"
+    for b in (0, 17, B - 1):
+        ref = attention_f64(q[b], k[b], v[b], t, t, H, dm)
+        assert maxerr(got[b], ref) <= TOL16, f"window {b}"
+
+
 def test_fused_qkv_row_layout(wrs, ctx):
     # q/k/v as column slices of one [B][T][3*d_model] projection output
     # (crates/whisper/src/encoder.rs:275-287) give the same bits as packed rows.
