@@ -140,6 +140,44 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
     return cfg, us, gbs
 
 
+def bench_host_slice(wrs, W, ctx, reps=20):
+    """The host-slice drop-in (flash_attention_2 on f32 host slices, PCIe both
+    ways) against the same call on device-resident f32 tensors, whisper-tiny
+    encoder shape. Informational: never the headline value."""
+    import torch
+    cfg = W.TINY_ENCODER
+    q, k, v = (np.ascontiguousarray(x[0]) for x in cfg.inputs())
+    out = np.empty_like(q)
+    T, H, dm = cfg.t, cfg.n_heads, cfg.d_model
+    for _ in range(3):
+        wrs.flash_attention_2(q, k, v, T, T, H, dm, False, out, ctx=ctx)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        wrs.flash_attention_2(q, k, v, T, T, H, dm, False, out, ctx=ctx)
+    host_ms = (time.perf_counter() - t0) * 1e3 / reps
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+    od = torch.empty_like(qd)
+    lay = wrs.token_major(T, dm, 64)
+    run = lambda: wrs.prefill(qd, kd, vd, od, batch=1, n_heads=H, t_q=T, t_kv=T, d_head=64,
+                              q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+    for _ in range(20):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    e1.synchronize()
+    dev_ms = e0.elapsed_time(e1) / reps
+    gflop = cfg.flops() / 1e9
+    return {"workload": cfg.name, "unit": "GFLOP/s",
+            "host_slice_ms": round(host_ms, 3), "host_slice_value": round(gflop / host_ms * 1e3, 1),
+            "device_resident_ms": round(dev_ms, 4),
+            "device_resident_value": round(gflop / dev_ms * 1e3, 1),
+            "pcie_bytes_per_call": 4 * q.nbytes}
+
+
 def copy_bandwidth():
     import torch
     n = 1 << 28  # 1 GiB of f32
@@ -288,6 +326,8 @@ def main():
         return
     cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
+    log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
+    host_slice = bench_host_slice(wrs, W, ctx)
     copy_gbs = copy_bandwidth()
 
     enc_traffic = dec_traffic = None
@@ -335,6 +375,7 @@ def main():
                          "traffic": traffic_bytes(dec_traffic)},
             "cpu_baseline": cpu_dec,
         },
+        "host_slice": host_slice,
         "device": {"name": props.name, "cu": props.multi_processor_count,
                    "copy_GBps": round(copy_gbs, 1)},
     }
