@@ -140,6 +140,58 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
     return cfg, us, gbs
 
 
+def bench_capture(wrs, W, ctx, reps, use_graph=True):
+    """DTW alignment pass: one capture launch per preset layer, inputs resident."""
+    import torch
+    cfg = W.LARGE_DTW_CAPTURE
+    layers = cfg.layers()
+    ar = wrs.KvArena(cfg.n_layers, 1, cfg.n_heads, 448, cfg.n_audio, ctx=ctx)
+    zeros = torch.zeros((cfg.n_audio, cfg.d_model), device="cuda")
+    for layer in layers:
+        ar.set_cross(layer, torch.from_numpy(cfg.k(layer)).cuda(), zeros)
+    qs = {layer: torch.from_numpy(cfg.q(layer)).cuda() for layer in layers}
+    n_sel = len(cfg.heads)
+    out = torch.zeros(cfg.n_tokens * n_sel * cfg.n_audio, device="cuda")
+
+    def all_layers():
+        for layer in layers:
+            ar.capture_cross_heads(layer, qs[layer], cfg.pairs(layer), n_sel, 0, out)
+
+    all_layers()
+    torch.cuda.synchronize()
+    if not use_graph:
+        for _ in range(reps):
+            all_layers()
+        torch.cuda.synchronize()
+        ar.close()
+        return cfg, float("nan"), float("nan")
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.use_torch_stream()
+        all_layers()
+    ctx.use_torch_stream()
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(out, eager):
+        raise RuntimeError("graph replay of the capture launches differs from eager")
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"capture: timing {reps} graph replays of {len(layers)} launches")
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (reps * len(layers))
+    gbs = cfg.bytes_per_pair() / (us * 1e-6) / 1e9  # one pair per preset layer
+    ar.close()
+    return cfg, us, gbs
+
+
 def bench_host_slice(wrs, W, ctx, reps=20):
     """The host-slice drop-in (flash_attention_2 on f32 host slices, PCIe both
     ways) against the same call on device-resident f32 tensors, whisper-tiny
@@ -208,7 +260,7 @@ def calibration_copy():
 
 
 def measure_traffic(only: str, kernel_tag: str, extra: list[str]):
-    """HBM bytes per launch of the kernel whose name contains kernel_tag.
+    """HBM bytes per call of the kernel(s) whose name contains kernel_tag.
 
     Two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch)
     over `bench.py --only <only>`; each counter is scaled by what it reads for
@@ -239,10 +291,13 @@ def measure_traffic(only: str, kernel_tag: str, extra: list[str]):
                 log(f"traffic: {counter}: kernels not found in the profile")
                 return None
             factor = CALIB_BYTES / (max(copy) * 1024.0)
-            out[counter] = kern[0] * 1024.0 * factor
+            # one call of the path = one dispatch of each matching kernel
+            # (the capture runs as two passes)
+            out[counter] = sum(kern) * 1024.0 * factor
             out[counter + "_factor"] = factor
-            log(f"traffic: {only} {counter} = {kern[0]:.1f} KiB/dispatch, copy of "
-                f"{CALIB_BYTES} B reads {max(copy):.1f} KiB -> factor {factor:.4f}")
+            log(f"traffic: {only} {counter} = {sum(kern):.1f} KiB per call over {len(kern)} "
+                f"kernel(s), copy of {CALIB_BYTES} B reads {max(copy):.1f} KiB -> "
+                f"factor {factor:.4f}")
     return out
 
 
@@ -286,6 +341,26 @@ def cpu_baseline_decode(cfg):
                       f"{best * 1e3:.2f} ms"}
 
 
+def cpu_baseline_capture(cfg):
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    layer = cfg.layers()[0]
+    q = np.ascontiguousarray(cfg.q(layer).ravel())
+    k = np.ascontiguousarray(cfg.k(layer).ravel())
+    sel = cfg.pairs(layer)
+    out = np.zeros(cfg.n_tokens * len(cfg.heads) * cfg.n_audio, np.float32)
+    best = float("inf")
+    for _ in range(5):
+        t0 = time.perf_counter()
+        orc.capture_cross_attention_heads(q, k, cfg.n_tokens, cfg.n_audio, cfg.n_heads,
+                                          cfg.d_model, sel, len(cfg.heads), 0, out)
+        best = min(best, time.perf_counter() - t0)
+    return {"value": cfg.bytes_per_pair() / best / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"1 layer's pair ({cfg.n_tokens} tokens x {cfg.n_audio} frames), best of 5, "
+                      f"{best * 1e3:.2f} ms"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,7 +373,8 @@ def main():
                     help="with --only decode: plain launches instead of a graph replay")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 HBM-traffic passes")
-    ap.add_argument("--only", choices=["encoder", "decode"], default=None,
+    ap.add_argument("--capture-reps", type=int, default=100)
+    ap.add_argument("--only", choices=["encoder", "decode", "capture"], default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -324,28 +400,38 @@ def main():
         calibration_copy()
         log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
         return
+    if args.only == "capture":
+        _, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps, use_graph=not args.eager)
+        calibration_copy()
+        log(f"capture only: {cus:.3f} us/launch, {cgbs:.1f} GB/s")
+        return
     cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
+    ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
     log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
     host_slice = bench_host_slice(wrs, W, ctx)
     copy_gbs = copy_bandwidth()
 
-    enc_traffic = dec_traffic = None
+    enc_traffic = dec_traffic = cap_traffic = None
     if not args.no_traffic:
         log("traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes")
         enc_traffic = measure_traffic("encoder", "fa2_prefill", ["--steps", "3", "--warmup", "1"])
         dec_traffic = measure_traffic("decode", "decode_f16", ["--decode-reps", "3", "--eager"])
+        cap_traffic = measure_traffic("capture", "capture_cross", ["--capture-reps", "3",
+                                                                    "--eager"])
 
     def traffic_bytes(t):
         return None if t is None else round(t["FETCH_SIZE"] + t["WRITE_SIZE"])
 
     threads = min(16, os.cpu_count() or 1)
-    cpu_enc = cpu_dec = None
+    cpu_enc = cpu_dec = cpu_cap = None
     if not args.no_cpu:
         log(f"cpu baseline: oracle encoder window on {threads} threads")
         cpu_enc = cpu_baseline_encoder(cfg, qkv, threads)
         log("cpu baseline: oracle decode layer, 1 thread")
         cpu_dec = cpu_baseline_decode(dcfg)
+        log("cpu baseline: oracle capture of one layer, 1 thread")
+        cpu_cap = cpu_baseline_capture(ccfg)
 
     line = {
         "metric": METRIC,
@@ -374,6 +460,15 @@ def main():
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic_bytes(dec_traffic)},
             "cpu_baseline": cpu_dec,
+        },
+        "capture": {
+            "workload": ccfg.name, "value": round(cgbs, 1), "unit": "GB/s",
+            "us_per_launch": round(cus, 3), "launches_per_step": len(ccfg.layers()),
+            "bytes_per_launch": ccfg.bytes_per_pair(), "dtype": "f32",
+            "roofline": {"bound": "hbm", "achieved": round(cgbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(cgbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic_bytes(cap_traffic)},
+            "cpu_baseline": cpu_cap,
         },
         "host_slice": host_slice,
         "device": {"name": props.name, "cu": props.multi_processor_count,

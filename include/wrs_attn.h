@@ -180,6 +180,20 @@ int wrs_attn_prefill_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, size_t sl
 int wrs_attn_prefill_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
                            size_t n_tokens, float *out);
 
+/* ---- alignment-head capture (asynchronous) -----------------------------
+ * fn capture_cross_attention_heads(q, k, n_tokens, n_audio, n_heads, d_model,
+ * selected, n_selected, row_offset, out, scores) -- decoder.rs:796-828, as
+ * called per text layer from decoder.rs:709-721. k is this layer's cross
+ * plane of the arena (n_audio = wrs_kv_cross_len); selected is given as two
+ * host arrays, pair p = (slots[p], heads[p]). q: [n_tokens][d_model] f32
+ * device, 16-byte aligned; out: f32 device buffer of out_len elements,
+ * written at [(row_offset + i) * n_selected + slots[p]][0..n_audio). The
+ * reference's scores scratch is internal (chunk statistics in the context). */
+int wrs_attn_capture_cross_heads(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
+                                 size_t n_tokens, const size_t *slots, const size_t *heads,
+                                 size_t n_pairs, size_t n_selected, size_t row_offset,
+                                 float *out, size_t out_len);
+
 #ifdef __cplusplus
 }
 #endif

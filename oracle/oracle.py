@@ -2,7 +2,7 @@
 
 The oracle is a C restatement of the reference's CPU attention path
 (crates/tensor/src/ops/attention.rs, crates/tensor/src/ops/softmax.rs,
-crates/tensor/src/simd.rs:4-119, crates/whisper/src/decoder.rs:835-892).
+crates/tensor/src/simd.rs:4-119, crates/whisper/src/decoder.rs:796-892).
 Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
 import this module, and only as the checker or the timed CPU baseline. The
 product package (``whisper.rs_amd``) never imports it.
@@ -58,6 +58,10 @@ def lib() -> ctypes.CDLL:
         L.wrs_oracle_mha_with_cache.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
                                                 _f32p]
         L.wrs_oracle_mha_with_cache.restype = ctypes.c_int
+        _szp = ctypes.POINTER(_sz)
+        L.wrs_oracle_capture_cross_heads.argtypes = [_f32p, _f32p, _sz, _sz, _sz, _sz, _szp, _szp,
+                                                     _sz, _sz, _sz, _f32p]
+        L.wrs_oracle_capture_cross_heads.restype = ctypes.c_int
         L.wrs_oracle_xorshift_fill.argtypes = [ctypes.POINTER(ctypes.c_uint32), _f32p, _sz]
         L.wrs_oracle_xorshift_fill.restype = None
         L.wrs_oracle_uses_avx2.argtypes = []
@@ -144,6 +148,26 @@ def mha_with_cache(q, k, v, n_tokens, total_tokens, t_past, n_heads, d_model, ou
     rc = lib().wrs_oracle_mha_with_cache(_ptr(q), _ptr(k), _ptr(v), n_tokens, total_tokens,
                                          t_past, n_heads, d_model, _ptr(output))
     _check(rc, "multi_head_attention_with_cache")
+
+
+def capture_cross_attention_heads(q, k, n_tokens, n_audio, n_heads, d_model, selected,
+                                  n_selected, row_offset, out):
+    """crates/whisper/src/decoder.rs:796-828; ``selected`` is [(slot, head), ...]."""
+    assert n_heads > 0 and d_model % n_heads == 0
+    assert q.size >= n_tokens * d_model and k.size >= n_audio * d_model
+    assert out.size >= (row_offset + n_tokens) * n_selected * n_audio  # decoder.rs:812
+    d_head = d_model // n_heads
+    for slot, head in selected:
+        assert (head + 1) * d_head <= d_model  # the q/k slices of decoder.rs:815-817
+        assert ((row_offset + n_tokens - 1) * n_selected + slot + 1) * n_audio <= out.size or \
+            n_tokens == 0
+    n = len(selected)
+    slots = (ctypes.c_size_t * max(n, 1))(*[s for s, _ in selected])
+    heads = (ctypes.c_size_t * max(n, 1))(*[h for _, h in selected])
+    rc = lib().wrs_oracle_capture_cross_heads(_ptr(q), _ptr(k), n_tokens, n_audio, n_heads,
+                                              d_model, slots, heads, n, n_selected, row_offset,
+                                              _ptr(out))
+    _check(rc, "capture_cross_attention_heads")
 
 
 def uses_avx2() -> bool:

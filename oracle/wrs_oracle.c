@@ -12,6 +12,7 @@
  *   crates/tensor/src/ops/softmax.rs     softmax_inplace
  *   crates/tensor/src/simd.rs:4-119      dot_f32 (AVX2+FMA and scalar)
  *   crates/whisper/src/decoder.rs:835-892 multi_head_attention_with_cache
+ *   crates/whisper/src/decoder.rs:796-828 capture_cross_attention_heads
  *   crates/tensor/tests/test_flash_attention_tiled.rs:15-35 xorshift32 inputs
  *
  * What pins each function (checked in tests/test_oracle.py):
@@ -30,6 +31,11 @@
  *                          scalar body, softmax-weights of 1e-7 skip rule.
  *   mha_with_cache         materialized causal-with-offset reference; n=1
  *                          dispatch equals single_token_mha_d64 bitwise.
+ *   capture_cross_heads    f64 softmax of the head's scores (1e-6) with the
+ *                          [row][slot][n_audio] placement, the reference
+ *                          test's row checks (test_dtw_alignment.rs:60-74),
+ *                          K == 0 -> exactly fl(1/n_audio), dominant key,
+ *                          and weights x V == multi_head_attention per head.
  * Bitwise equality with the Rust binary is NOT pinned for the tiled path: the
  * reference's two matrix products run in matrixmultiply 0.3.11 sgemm
  * (Cargo.lock:257-260), which is not vendored under the reference tree. Its
@@ -484,6 +490,39 @@ int wrs_oracle_mha_with_cache(const float *q, const float *k, const float *v,
                 const float *v_vec = v + j * d_model + head_offset;
                 for (size_t d = 0; d < d_head; ++d) out_vec[d] += w * v_vec[d];
             }
+        }
+    }
+    free(scores);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* decoder.rs:796-828 capture_cross_attention_heads                          */
+/* ------------------------------------------------------------------------ */
+/* Softmax cross-attention weights of the selected heads: for row i and pair
+ * (slot, head), scores_j = dot_f32(q_i[head], k_j[head]) * scale over the
+ * n_audio keys (:815-818), softmax_inplace (:819), copied to
+ * out[((row_offset + i) * n_selected + slot) * n_audio ..] (:821-822). */
+int wrs_oracle_capture_cross_heads(const float *q, const float *k, size_t n_tokens,
+                                   size_t n_audio, size_t n_heads, size_t d_model,
+                                   const size_t *slots, const size_t *heads, size_t n_pairs,
+                                   size_t n_selected, size_t row_offset, float *out) {
+    if (n_heads == 0) return -1;
+    if (d_model % n_heads != 0) return -2;
+    size_t d_head = d_model / n_heads;
+    const float scale = 1.0f / sqrtf((float)d_head); /* :810 */
+    float *scores = (float *)malloc(sizeof(float) * (n_audio ? n_audio : 1));
+    if (!scores) return -12;
+    for (size_t i = 0; i < n_tokens; ++i) {
+        for (size_t p = 0; p < n_pairs; ++p) {
+            size_t head_offset = heads[p] * d_head;
+            const float *q_vec = q + i * d_model + head_offset;
+            for (size_t j = 0; j < n_audio; ++j)
+                scores[j] = wrs_oracle_dot_f32(q_vec, k + j * d_model + head_offset, d_head) *
+                            scale;
+            wrs_oracle_softmax_inplace(scores, n_audio);
+            float *dst = out + ((row_offset + i) * n_selected + slots[p]) * n_audio;
+            memcpy(dst, scores, sizeof(float) * n_audio);
         }
     }
     free(scores);

@@ -56,6 +56,13 @@ int wrs_oracle_mha_with_cache(const float *q, const float *k, const float *v,
                               size_t t_past, size_t n_heads, size_t d_model,
                               float *out);
 
+/* decoder.rs:796-828: softmax cross-attention weights of selected heads,
+ * out[((row_offset + i) * n_selected + slots[p]) * n_audio + j]. */
+int wrs_oracle_capture_cross_heads(const float *q, const float *k, size_t n_tokens,
+                                   size_t n_audio, size_t n_heads, size_t d_model,
+                                   const size_t *slots, const size_t *heads, size_t n_pairs,
+                                   size_t n_selected, size_t row_offset, float *out);
+
 /* xorshift32 generator of crates/tensor/tests/test_flash_attention_tiled.rs:15-35.
  * Fills out[0..n) and advances *state. */
 void wrs_oracle_xorshift_fill(uint32_t *state, float *out, size_t n);

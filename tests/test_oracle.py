@@ -328,3 +328,95 @@ def test_mha_with_cache_single_token_dispatch(orc):
     orc.mha_with_cache(q, k, v, 1, t_past + 1, t_past, n_heads, d_model, a)
     orc.single_token_mha_d64(q, k, v, t_past + 1, n_heads, d_model, b)
     np.testing.assert_array_equal(a, b)
+
+
+# ---- capture_cross_attention_heads (crates/whisper/src/decoder.rs:796-828) ----
+
+def _capture_f64(q, k, n_tokens, n_audio, n_heads, d_model, head):
+    dh = d_model // n_heads
+    qh = q.reshape(n_tokens, d_model)[:, head * dh:(head + 1) * dh].astype(np.float64)
+    kh = k.reshape(n_audio, d_model)[:, head * dh:(head + 1) * dh].astype(np.float64)
+    s = qh @ kh.T / np.sqrt(dh)
+    e = np.exp(s - s.max(axis=1, keepdims=True))
+    return e / e.sum(axis=1, keepdims=True)
+
+
+@pytest.mark.parametrize("n_audio", [1, 37, 1500])
+def test_capture_against_f64_and_layout(orc, n_audio):
+    n_tokens, H, dm, n_sel, row_off = 3, 4, 256, 3, 2
+    rng = np.random.default_rng(n_audio)
+    q = rng.standard_normal(n_tokens * dm).astype(np.float32)
+    k = rng.standard_normal(n_audio * dm).astype(np.float32)
+    selected = [(2, 1), (0, 3)]  # (slot, head); slot 1 belongs to another layer
+    out = np.full((row_off + n_tokens) * n_sel * n_audio, np.nan, np.float32)
+    orc.capture_cross_attention_heads(q, k, n_tokens, n_audio, H, dm, selected, n_sel, row_off,
+                                      out)
+    o = out.reshape(row_off + n_tokens, n_sel, n_audio)
+    for slot, head in selected:
+        ref = _capture_f64(q, k, n_tokens, n_audio, H, dm, head)
+        assert np.abs(o[row_off:, slot] - ref).max() <= 1e-6
+    # rows before row_offset and the slot of no pair stay untouched (decoder.rs:821)
+    assert np.isnan(o[:row_off]).all() and np.isnan(o[:, 1]).all()
+
+
+def test_capture_rows_are_distributions(orc):
+    """crates/whisper/tests/test_dtw_alignment.rs:60-74: finite, >= 0, rows sum to 1 +- 1e-4."""
+    n_tokens, n_audio, H, dm = 5, 1500, 6, 384  # tiny.en width
+    rng = np.random.default_rng(7)
+    q = (3.0 * rng.standard_normal(n_tokens * dm)).astype(np.float32)
+    k = rng.standard_normal(n_audio * dm).astype(np.float32)
+    selected = list(enumerate([1, 2, 3, 5]))
+    out = np.zeros(n_tokens * len(selected) * n_audio, np.float32)
+    orc.capture_cross_attention_heads(q, k, n_tokens, n_audio, H, dm, selected, len(selected), 0,
+                                      out)
+    assert np.isfinite(out).all() and (out >= 0).all()
+    sums = out.reshape(-1, n_audio).astype(np.float64).sum(axis=1)
+    assert np.abs(sums - 1.0).max() < 1e-4
+
+
+def test_capture_zero_keys_are_uniform(orc):
+    """K == 0: every score is 0, exp(0) = 1, the sum is n exactly, weight = fl(1/n)."""
+    n_tokens, n_audio, H, dm = 2, 1500, 2, 128
+    q = np.random.default_rng(1).standard_normal(n_tokens * dm).astype(np.float32)
+    k = np.zeros(n_audio * dm, np.float32)
+    out = np.zeros(n_tokens * n_audio, np.float32)
+    orc.capture_cross_attention_heads(q, k, n_tokens, n_audio, H, dm, [(0, 1)], 1, 0, out)
+    assert (out == np.float32(1.0) / np.float32(n_audio)).all()
+
+
+def test_capture_dominant_key(orc):
+    """One key aligned with q at a large margin takes all the weight."""
+    n_audio, H, dm = 300, 4, 256
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal(dm).astype(np.float32)
+    k = (0.01 * rng.standard_normal(n_audio * dm)).astype(np.float32).reshape(n_audio, dm)
+    k[123, 64:128] = 40.0 * q[64:128] / np.linalg.norm(q[64:128])
+    out = np.zeros(n_audio, np.float32)
+    orc.capture_cross_attention_heads(q, k.ravel().copy(), 1, n_audio, H, dm, [(0, 1)], 1, 0, out)
+    assert out.argmax() == 123 and out[123] > 0.999
+
+
+def test_capture_weights_reproduce_attention(orc):
+    """Weights of head h times V[:, h] equal multi_head_attention's head-h output
+    (attention.rs:29-41, pinned above): ties the scale and head offset to it."""
+    n_tokens, n_audio, H, dm = 4, 211, 4, 256
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(n_tokens * dm).astype(np.float32)
+    k = rng.standard_normal(n_audio * dm).astype(np.float32)
+    v = rng.standard_normal(n_audio * dm).astype(np.float32)
+    att = np.zeros(n_tokens * dm, np.float32)
+    orc.multi_head_attention(q, k, v, n_tokens, n_audio, H, dm, False, att)
+    selected = [(h, h) for h in range(H)]
+    out = np.zeros(n_tokens * H * n_audio, np.float32)
+    orc.capture_cross_attention_heads(q, k, n_tokens, n_audio, H, dm, selected, H, 0, out)
+    w = out.reshape(n_tokens, H, n_audio).astype(np.float64)
+    vv = v.reshape(n_audio, H, 64).astype(np.float64)
+    got = np.einsum("thj,jhd->thd", w, vv).reshape(n_tokens, dm)
+    assert np.abs(got - att.reshape(n_tokens, dm)).max() <= 1e-5
+
+
+def test_capture_empty_audio_is_noop(orc):
+    out = np.full(6, 7.0, np.float32)
+    orc.capture_cross_attention_heads(np.ones(128, np.float32), np.zeros(0, np.float32), 1, 0, 2,
+                                      128, [(0, 0)], 1, 0, out)
+    assert (out == 7.0).all()

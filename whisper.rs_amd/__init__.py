@@ -12,7 +12,8 @@ Host-side mirror of the reference's attention interface over the C ABI of
 * device-resident entry points on torch tensors (torch supplies device memory
   and the stream; every FLOP runs in this package's HIP kernels):
   ``prefill`` and the ``KvArena`` (DecoderKvCache, decoder.rs:131-264) with
-  its ``decode_self`` / ``decode_cross`` / ``prefill_self`` / ``prefill_cross``.
+  its ``decode_self`` / ``decode_cross`` / ``prefill_self`` / ``prefill_cross``
+  and the DTW alignment-head capture ``capture_cross_heads``.
 
 There is no CPU fallback: without the built library every call raises.
 """
@@ -302,3 +303,17 @@ class KvArena:
         self._c(self._lib.wrs_attn_prefill_cross(self.ctx.handle, self.handle, layer,
                                                  q.data_ptr(), q.shape[0], out.data_ptr()),
                 "prefill_cross")
+
+    def capture_cross_heads(self, layer, q, selected, n_selected, row_offset, out):
+        """capture_cross_attention_heads (crates/whisper/src/decoder.rs:796-828).
+
+        ``selected`` lists this layer's (slot, head) pairs; ``q`` is the
+        layer's [n_tokens][d_model] float32 query tensor and ``out`` the float32
+        capture buffer laid out [row][slot][n_audio] (decoder.rs:821-822).
+        """
+        n = len(selected)
+        slots = (ctypes.c_size_t * max(n, 1))(*[s for s, _ in selected])
+        heads = (ctypes.c_size_t * max(n, 1))(*[h for _, h in selected])
+        self._c(self._lib.wrs_attn_capture_cross_heads(
+            self.ctx.handle, self.handle, layer, q.data_ptr(), q.shape[0], slots, heads, n,
+            n_selected, row_offset, out.data_ptr(), out.numel()), "capture_cross_heads")

@@ -76,6 +76,8 @@ _SIGNATURES = {
     "wrs_attn_decode_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_self": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "wrs_attn_capture_cross_heads": (_int, [_vp, _vp, _sz, _vp, _sz, _szp, _szp, _sz, _sz, _sz,
+                                            _vp, _sz]),
 }
 
 _lib = None

@@ -30,6 +30,8 @@ struct wrs_attn_ctx {
   size_t part_bytes = 0;
   unsigned* counters = nullptr;  // decode merge counters (kept zero between launches)
   size_t counter_bytes = 0;
+  float* cap_part = nullptr;  // alignment-head capture chunk statistics
+  size_t cap_part_bytes = 0;
 };
 
 struct wrs_kv {
@@ -310,6 +312,7 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
   if (c->stage) (void)hipFree(c->stage);
   if (c->part) (void)hipFree(c->part);
   if (c->counters) (void)hipFree(c->counters);
+  if (c->cap_part) (void)hipFree(c->cap_part);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -811,6 +814,63 @@ int wrs_attn_prefill_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const floa
   const uint16_t* vb = kv->v_cross + kv->cross_off(layer);
   return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
                       n_tokens, kv->cross_len[layer], 64, 0, 0);
+}
+
+int wrs_attn_capture_cross_heads(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                                 size_t n_tokens, const size_t* slots, const size_t* heads,
+                                 size_t n_pairs, size_t n_selected, size_t row_offset, float* out,
+                                 size_t out_len) {
+  if (!c || !kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n_tokens == 0 || n_pairs == 0) return WRS_OK;
+  if (!q || !out || !slots || !heads) return fail(c, WRS_EINVAL, "null argument");
+  for (size_t p = 0; p < n_pairs; ++p) {
+    // decoder.rs:814-816 slices q/k at head * d_head (panics past d_model);
+    // the slot comes from enumerating the caller's head list (decoder.rs:683).
+    if (heads[p] >= kv->n_heads) return fail(c, WRS_EINVAL, "head index >= n_heads");
+    if (slots[p] >= n_selected) return fail(c, WRS_EINVAL, "slot index >= n_selected");
+  }
+  const size_t n_audio = kv->cross_len[layer];
+  // decoder.rs:812 / :822: out holds (row_offset + n_tokens) rows of
+  // n_selected * n_audio weights.
+  if (out_len / std::max<size_t>(1, n_selected * n_audio) < row_offset + n_tokens &&
+      n_audio > 0)
+    return fail(c, WRS_EINVAL, "out shorter than (row_offset + n_tokens) * n_selected * n_audio");
+  if (n_audio == 0) return WRS_OK;  // softmax of an empty row (softmax.rs:2-4)
+  if ((reinterpret_cast<uintptr_t>(q) & 15) != 0)
+    return fail(c, WRS_EINVAL, "q must be 16-byte aligned");
+  if (n_tokens > static_cast<size_t>(65535) * wrs::kCaptureRows ||
+      (row_offset + n_tokens) * n_selected > static_cast<size_t>(INT32_MAX))
+    return fail(c, WRS_EINVAL, "capture shape too large");
+  DeviceGuard g(c->device);
+  wrs::CaptureArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const _Float16*>(kv->k_cross + kv->cross_off(layer));
+  a.out = out;
+  a.q_rs = static_cast<int64_t>(kv->d_model());
+  a.kv_hs = static_cast<int64_t>(kv->n_audio_max * 64);
+  a.n_tokens = static_cast<int>(n_tokens);
+  a.n_audio = static_cast<int>(n_audio);
+  a.n_selected = static_cast<int>(n_selected);
+  a.row_offset = static_cast<int>(row_offset);
+  a.scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) (decoder.rs:810) * log2(e)
+  const size_t pb =
+      wrs::capture_part_floats(static_cast<int>(std::min<size_t>(n_pairs, wrs::kMaxCapturePairs)),
+                               a.n_tokens, a.n_audio) * sizeof(float);
+  int rc = grow(c, reinterpret_cast<void**>(&c->cap_part), &c->cap_part_bytes, pb, false);
+  if (rc) return rc;
+  a.part = c->cap_part;
+  for (size_t p0 = 0; p0 < n_pairs; p0 += wrs::kMaxCapturePairs) {
+    const size_t np = std::min<size_t>(wrs::kMaxCapturePairs, n_pairs - p0);
+    a.n_pairs = static_cast<int>(np);
+    for (size_t p = 0; p < np; ++p) {
+      a.slot[p] = static_cast<int>(slots[p0 + p]);
+      a.head[p] = static_cast<int>(heads[p0 + p]);
+    }
+    WRS_HIP(c, wrs::launch_capture_cross_f16(a, c->stream));
+  }
+  return WRS_OK;
 }
 
 }  // extern "C"

@@ -86,6 +86,27 @@ hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s);
 size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows);
 size_t decode_counter_words(int n_groups, int n_heads);
 
+// Alignment-head capture over the f16 cross plane
+// (decoder.rs:796-828 semantics): for query row i and pair p,
+// softmax_j(dot(q_i[head_p], k_j[head_p]) * scale) into
+// out[((row_offset + i) * n_selected + slot_p) * n_audio + j].
+constexpr int kCaptureRows = 16;       // query rows per workgroup
+constexpr int kCaptureChunk = 128;     // keys per workgroup
+constexpr int kMaxCapturePairs = 32;   // (slot, head) pairs per launch
+struct CaptureArgs {
+  const float* q;     // row i, head h: q + i*q_rs + h*64
+  const _Float16* k;  // plane of head h: k + h*kv_hs, key j at +j*64
+  float* out;
+  float* part;        // scratch: capture_part_floats(n_pairs, n_tokens, n_audio)
+  int64_t q_rs, kv_hs;
+  int n_tokens, n_audio, n_selected, row_offset, n_pairs;
+  float scale_log2;  // log2(e)/sqrt(64): decoder.rs:810's scale in the exp2 domain
+  int slot[kMaxCapturePairs];
+  int head[kMaxCapturePairs];
+};
+size_t capture_part_floats(int n_pairs, int n_tokens, int n_audio);
+hipError_t launch_capture_cross_f16(const CaptureArgs& a, hipStream_t s);
+
 // KV arena kernels.
 // f32 rows [n][d_model] (row stride src_rs) -> f16 planes: head h, row i at
 // dst + h*dst_hs + (pos + i)*64.

@@ -134,6 +134,44 @@ class SelfDecode:
         return k, v
 
 
+@dataclass(frozen=True)
+class AlignmentCapture:
+    """DTW alignment pass of one segment: the cross-attention weights of the
+    preset's (text layer, head) pairs for every token of the segment."""
+
+    name: str
+    n_tokens: int
+    n_heads: int
+    n_audio: int
+    n_layers: int
+    heads: tuple  # ((layer, head), ...)
+
+    @property
+    def d_model(self) -> int:
+        return self.n_heads * 64
+
+    def layers(self) -> list[int]:
+        return sorted({l for l, _ in self.heads})
+
+    def pairs(self, layer: int) -> list[tuple[int, int]]:
+        return [(slot, h) for slot, (l, h) in enumerate(self.heads) if l == layer]
+
+    def bytes_per_pair(self) -> int:
+        # the head's f16 K plane, its f32 query slices, the f32 weights written
+        return (self.n_audio * 64 * 2 + self.n_tokens * 64 * 4
+                + self.n_tokens * self.n_audio * 4)
+
+    def q(self, layer: int) -> np.ndarray:
+        return normal((self.n_tokens, self.d_model), 500 + layer)
+
+    def k(self, layer: int) -> np.ndarray:
+        return normal((self.n_audio, self.d_model), 3000 + layer, storage="f16")
+
+
+# crates/whisper/src/dtw.rs AlignmentHeadsPreset::LargeV3
+LARGE_V3_ALIGNMENT_HEADS = ((7, 0), (10, 17), (12, 18), (13, 12), (16, 1), (17, 14), (19, 11),
+                            (21, 4), (24, 1), (25, 6))
+
 TINY_ENCODER = Encoder("whisper-tiny encoder self-attention, f32", 1, 6, 1500, "f32",
                        qk_prescale=64.0 ** -0.25)
 BASE_ENCODER = Encoder("whisper-base encoder self-attention x4 windows, f16", 4, 8, 1500, "f16")
@@ -143,3 +181,6 @@ LARGE_CROSS_DECODE = CrossDecode("whisper-large-v3 cross-attention decode, beam 
 LARGE_ENCODER = Encoder("whisper-large-v3 encoder self-attention x16 windows, bf16 outliers", 16,
                         20, 1500, "bf16", sigma=0.5, outliers=13)
 SELF_DECODE_SWEEP = (32, 64, 128, 224, 256, 384, 448)
+# 124 text tokens + SOT, language, NOT and EOT (transcribe.rs:1403-1411)
+LARGE_DTW_CAPTURE = AlignmentCapture("whisper-large-v3 DTW alignment-head capture, 128 tokens",
+                                     128, 20, 1500, 32, LARGE_V3_ALIGNMENT_HEADS)
