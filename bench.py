@@ -192,6 +192,29 @@ def bench_capture(wrs, W, ctx, reps, use_graph=True):
     return cfg, us, gbs
 
 
+def bench_linear(wrs, cfg, ctx, reps):
+    """One fused QKV projection per step, inputs resident; bf16 rows out."""
+    import torch
+    x = torch.from_numpy(cfg.x()).cuda()
+    if cfg.x_storage == "f16":
+        x = x.half()
+    w = torch.from_numpy(cfg.w()).cuda()
+    b = torch.from_numpy(cfg.bias()).cuda()
+    out = torch.empty((cfg.n_tokens, cfg.n_out), dtype=torch.bfloat16, device="cuda")
+    for _ in range(3):
+        wrs.linear(x, w, b, out, ctx=ctx)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"linear: timing {reps} launches ({cfg.name})")
+    start.record()
+    for _ in range(reps):
+        wrs.linear(x, w, b, out, ctx=ctx)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return ms, cfg.flops() / (ms * 1e-3) / 1e12
+
+
 def bench_host_slice(wrs, W, ctx, reps=20):
     """The host-slice drop-in (flash_attention_2 on f32 host slices, PCIe both
     ways) against the same call on device-resident f32 tensors, whisper-tiny
@@ -374,7 +397,8 @@ def main():
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 HBM-traffic passes")
     ap.add_argument("--capture-reps", type=int, default=100)
-    ap.add_argument("--only", choices=["encoder", "decode", "capture"], default=None,
+    ap.add_argument("--linear-reps", type=int, default=20)
+    ap.add_argument("--only", choices=["encoder", "decode", "capture", "linear"], default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -399,6 +423,12 @@ def main():
         _, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps, use_graph=not args.eager)
         calibration_copy()
         log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
+        return
+    if args.only == "linear":
+        for cfg in (W.LARGE_QKV_F16, W.LARGE_QKV_F32):
+            lms, ltf = bench_linear(wrs, cfg, ctx, args.linear_reps)
+            log(f"linear only: {cfg.name}: {lms:.4f} ms, {ltf:.1f} TFLOP/s")
+        calibration_copy()
         return
     if args.only == "capture":
         _, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps, use_graph=not args.eager)

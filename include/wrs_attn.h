@@ -194,6 +194,33 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, co
                                  size_t n_pairs, size_t n_selected, size_t row_offset,
                                  float *out, size_t out_len);
 
+/* ---- projections with f16 weights (asynchronous) -----------------------
+ * LinearWeight::linear with F16 weights (crates/tensor/src/weight.rs:116-137
+ * -> crates/tensor/src/ops/quant.rs:415-473 f16_linear):
+ * out(t, r) = W[r] . x[t] + bias[r], W [n_out][n_in] f16 row-major (the ggml
+ * halves), bias f32 or NULL, x [n_tokens] rows of n_in (row stride in
+ * elements) as f32 (products kept exact) or f16. x_len and out_len are the
+ * buffers' lengths in elements, checked like the reference's length asserts
+ * (quant.rs:424-425). out(t, r) is written in
+ * out_dtype at out + t*out_row_stride + (r/64)*out_head_stride + r%64:
+ * out_head_stride = 64 gives the reference's token-major [t][n_out] rows
+ * (encoder.rs:275-277's fused QKV output, read in place by wrs_attn_prefill).
+ * All pointers are device pointers. n_in % 64 == 0, n_out % 4 == 0. */
+int wrs_linear(wrs_attn_ctx *ctx, int x_dtype, const void *x, size_t x_len,
+               int64_t x_row_stride, const void *w, const float *bias, size_t n_tokens,
+               size_t n_in, size_t n_out, int out_dtype, void *out, size_t out_len,
+               int64_t out_row_stride, int64_t out_head_stride);
+
+/* WhisperDecoder::precompute_cross_attn (crates/whisper/src/decoder.rs:423-447)
+ * straight into the arena: for every layer l, K = enc . w_k[l]^T and
+ * V = enc . w_v[l]^T + b_v[l] (b_v may be NULL, or hold NULL entries), stored
+ * as the f16 cross planes; every layer's cross length becomes n_audio. enc is
+ * [n_audio] rows of d_model (f32 or f16, device); w_k / w_v / b_v are host
+ * arrays of n_layers device pointers. */
+int wrs_kv_set_cross_proj(wrs_kv *kv, int x_dtype, const void *enc, size_t enc_len,
+                          int64_t enc_row_stride, size_t n_audio, const void *const *w_k,
+                          const void *const *w_v, const float *const *b_v);
+
 #ifdef __cplusplus
 }
 #endif

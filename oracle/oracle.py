@@ -2,7 +2,8 @@
 
 The oracle is a C restatement of the reference's CPU attention path
 (crates/tensor/src/ops/attention.rs, crates/tensor/src/ops/softmax.rs,
-crates/tensor/src/simd.rs:4-119, crates/whisper/src/decoder.rs:796-892).
+crates/tensor/src/simd.rs:4-119 and :593-700, crates/tensor/src/ops/quant.rs:343-473,
+crates/whisper/src/decoder.rs:796-892).
 Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
 import this module, and only as the checker or the timed CPU baseline. The
 product package (``whisper.rs_amd``) never imports it.
@@ -62,6 +63,14 @@ def lib() -> ctypes.CDLL:
         L.wrs_oracle_capture_cross_heads.argtypes = [_f32p, _f32p, _sz, _sz, _sz, _sz, _szp, _szp,
                                                      _sz, _sz, _sz, _f32p]
         L.wrs_oracle_capture_cross_heads.restype = ctypes.c_int
+        _u16p = ctypes.POINTER(ctypes.c_uint16)
+        L.wrs_oracle_dot_f16_f32.argtypes = [_u16p, _f32p, _sz]
+        L.wrs_oracle_dot_f16_f32.restype = ctypes.c_float
+        L.wrs_oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.wrs_oracle_f16_to_f32.restype = ctypes.c_float
+        L.wrs_oracle_f16_linear.argtypes = [_u16p, _sz, _sz, _f32p, _f32p, _sz, _f32p,
+                                            ctypes.c_int]
+        L.wrs_oracle_f16_linear.restype = ctypes.c_int
         L.wrs_oracle_xorshift_fill.argtypes = [ctypes.POINTER(ctypes.c_uint32), _f32p, _sz]
         L.wrs_oracle_xorshift_fill.restype = None
         L.wrs_oracle_uses_avx2.argtypes = []
@@ -168,6 +177,35 @@ def capture_cross_attention_heads(q, k, n_tokens, n_audio, n_heads, d_model, sel
                                               d_model, slots, heads, n, n_selected, row_offset,
                                               _ptr(out))
     _check(rc, "capture_cross_attention_heads")
+
+
+def _u16(a: np.ndarray):
+    assert a.dtype == np.float16 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+def f16_to_f32(bits: int) -> float:
+    return float(lib().wrs_oracle_f16_to_f32(bits))
+
+
+def dot_f16_f32(w: np.ndarray, x: np.ndarray) -> float:
+    """crates/tensor/src/simd.rs:593-700; w is float16 (the weight row's halves)."""
+    assert w.size == x.size  # simd.rs:594
+    return float(lib().wrs_oracle_dot_f16_f32(_u16(w), _ptr(x), x.size))
+
+
+def f16_linear(w, rows, cols, x, bias, num_tokens, output, n_threads=None):
+    """crates/tensor/src/ops/quant.rs:415-473 (LinearWeight::linear, weight.rs:116-137):
+    output[t * rows + r] = W[r] . x[t] + bias[r]; w is float16 [rows][cols]."""
+    assert x.size == num_tokens * cols  # quant.rs:424
+    assert output.size == num_tokens * rows  # quant.rs:425
+    if bias is not None:
+        assert bias.size == rows  # quant.rs:427
+    assert w.size == rows * cols  # quant.rs:440
+    rc = lib().wrs_oracle_f16_linear(_u16(w), rows, cols, _ptr(x),
+                                     None if bias is None else _ptr(bias), num_tokens,
+                                     _ptr(output), _threads(n_threads))
+    _check(rc, "f16_linear")
 
 
 def uses_avx2() -> bool:

@@ -13,6 +13,9 @@
  *   crates/tensor/src/simd.rs:4-119      dot_f32 (AVX2+FMA and scalar)
  *   crates/whisper/src/decoder.rs:835-892 multi_head_attention_with_cache
  *   crates/whisper/src/decoder.rs:796-828 capture_cross_attention_heads
+ *   crates/tensor/src/simd.rs:593-700    dot_f16_f32 (AVX2+F16C and scalar)
+ *   crates/tensor/src/ops/quant.rs:343-473 f16_linear (LinearWeight::linear
+ *                                        with f16 weights, weight.rs:116-137)
  *   crates/tensor/tests/test_flash_attention_tiled.rs:15-35 xorshift32 inputs
  *
  * What pins each function (checked in tests/test_oracle.py):
@@ -493,6 +496,108 @@ int wrs_oracle_mha_with_cache(const float *q, const float *k, const float *v,
         }
     }
     free(scores);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* simd.rs:593-700 dot_f16_f32, quant.rs:343-473 f16_linear                  */
+/* ------------------------------------------------------------------------ */
+/* IEEE binary16 -> binary32, exact (half::f16::to_f32 / vcvtph2ps). */
+static float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0x1Fu) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else if (exp != 0) {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    } else if (man == 0) {
+        bits = sign;
+    } else { /* subnormal: normalize */
+        int e = -1;
+        do { man <<= 1; ++e; } while (!(man & 0x400u));
+        bits = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+float wrs_oracle_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
+
+static float dot_f16_f32_scalar(const uint16_t *w, const float *x, size_t len) {
+    /* simd.rs:614-639 */
+    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+    size_t i = 0;
+    while (i + 4 <= len) {
+        acc0 += f16_to_f32(w[i]) * x[i];
+        acc1 += f16_to_f32(w[i + 1]) * x[i + 1];
+        acc2 += f16_to_f32(w[i + 2]) * x[i + 2];
+        acc3 += f16_to_f32(w[i + 3]) * x[i + 3];
+        i += 4;
+    }
+    float sum = (acc0 + acc1) + (acc2 + acc3);
+    for (; i < len; ++i) sum += f16_to_f32(w[i]) * x[i];
+    return sum;
+}
+
+#if WRS_HAVE_X86
+__attribute__((target("avx2,fma,f16c"))) static float dot_f16_f32_avx2(const uint16_t *w,
+                                                                       const float *x,
+                                                                       size_t len) {
+    /* simd.rs:641-700: four accumulators over 32-element blocks, their sum,
+     * then 8-element chunks, hsum, scalar tail. */
+    __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
+    __m256 acc2 = _mm256_setzero_ps(), acc3 = _mm256_setzero_ps();
+    size_t n_blocks = len / 32;
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint16_t *pw = w + b * 32;
+        const float *px = x + b * 32;
+        acc0 = _mm256_fmadd_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)pw)),
+                               _mm256_loadu_ps(px), acc0);
+        acc1 = _mm256_fmadd_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(pw + 8))),
+                               _mm256_loadu_ps(px + 8), acc1);
+        acc2 = _mm256_fmadd_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(pw + 16))),
+                               _mm256_loadu_ps(px + 16), acc2);
+        acc3 = _mm256_fmadd_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(pw + 24))),
+                               _mm256_loadu_ps(px + 24), acc3);
+    }
+    __m256 acc = _mm256_add_ps(_mm256_add_ps(acc0, acc1), _mm256_add_ps(acc2, acc3));
+    size_t i = n_blocks * 32;
+    for (; i + 8 <= len; i += 8)
+        acc = _mm256_fmadd_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(w + i))),
+                              _mm256_loadu_ps(x + i), acc);
+    float result = hsum256(acc);
+    for (; i < len; ++i) result += f16_to_f32(w[i]) * x[i];
+    return result;
+}
+#endif
+
+float wrs_oracle_dot_f16_f32(const uint16_t *w, const float *x, size_t len) {
+#if WRS_HAVE_X86
+    /* simd.rs:596-604: the AVX2 body needs avx2, fma and f16c */
+    if (wrs_oracle_uses_avx2() && __builtin_cpu_supports("f16c")) return dot_f16_f32_avx2(w, x, len);
+#endif
+    return dot_f16_f32_scalar(w, x, len);
+}
+
+/* output[t * rows + r] = dot_f16_f32(W[r], x[t]) + bias[r] (quant.rs:415-473;
+ * the single-token branch, quant.rs:343-413, computes the same per row). Rows
+ * run in parallel with no cross-row reduction, so the result does not depend
+ * on the thread count. */
+int wrs_oracle_f16_linear(const uint16_t *w, size_t rows, size_t cols, const float *x,
+                          const float *bias, size_t num_tokens, float *out, int n_threads) {
+    if (num_tokens == 0 || rows == 0 || cols == 0) return 0; /* quant.rs:430-432 */
+    int nt = n_threads > 0 ? n_threads : omp_get_num_procs();
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (long r = 0; r < (long)rows; ++r) {
+        const uint16_t *wr = w + (size_t)r * cols;
+        float b = bias ? bias[r] : 0.0f;
+        for (size_t t = 0; t < num_tokens; ++t) {
+            float dot = wrs_oracle_dot_f16_f32(wr, x + t * cols, cols);
+            out[t * rows + (size_t)r] = bias ? dot + b : dot;
+        }
+    }
     return 0;
 }
 

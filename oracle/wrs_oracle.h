@@ -63,6 +63,14 @@ int wrs_oracle_capture_cross_heads(const float *q, const float *k, size_t n_toke
                                    const size_t *slots, const size_t *heads, size_t n_pairs,
                                    size_t n_selected, size_t row_offset, float *out);
 
+/* simd.rs:593-700 dot_f16_f32 (f16 weights widened exactly, f32 x). */
+float wrs_oracle_dot_f16_f32(const uint16_t *w, const float *x, size_t len);
+float wrs_oracle_f16_to_f32(uint16_t h);
+/* quant.rs:415-473 f16_linear: out[t * rows + r] = W[r] . x[t] + bias[r]
+ * (bias may be NULL). n_threads <= 0 uses every core. */
+int wrs_oracle_f16_linear(const uint16_t *w, size_t rows, size_t cols, const float *x,
+                          const float *bias, size_t num_tokens, float *out, int n_threads);
+
 /* xorshift32 generator of crates/tensor/tests/test_flash_attention_tiled.rs:15-35.
  * Fills out[0..n) and advances *state. */
 void wrs_oracle_xorshift_fill(uint32_t *state, float *out, size_t n);

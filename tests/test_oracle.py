@@ -420,3 +420,78 @@ def test_capture_empty_audio_is_noop(orc):
     orc.capture_cross_attention_heads(np.ones(128, np.float32), np.zeros(0, np.float32), 1, 0, 2,
                                       128, [(0, 0)], 1, 0, out)
     assert (out == 7.0).all()
+
+
+# ---- f16_linear / dot_f16_f32 (crates/tensor/src/ops/quant.rs:415-473, simd.rs:593-700) ----
+
+def test_f16_to_f32_all_bit_patterns(orc):
+    """Every binary16 pattern widens exactly (numpy's conversion is IEEE exact)."""
+    bits = np.arange(65536, dtype=np.uint32)
+    got = np.array([orc.f16_to_f32(int(b)) for b in bits], np.float32)
+    ref = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [0, 1, 3, 8, 31, 32, 40, 64, 100, 1280])
+def test_dot_f16_exact_on_integers(orc, n):
+    rng = np.random.default_rng(n)
+    w = rng.integers(-8, 9, n).astype(np.float16)
+    x = rng.integers(-8, 9, n).astype(np.float32)
+    assert orc.dot_f16_f32(w, x) == float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+
+
+def test_dot_f16_scalar_and_avx2_agree_with_f64(orc):
+    rng = np.random.default_rng(5)
+    for n in (7, 33, 64, 391, 1280):
+        w = rng.standard_normal(n).astype(np.float16)
+        x = rng.standard_normal(n).astype(np.float32)
+        exact = float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+        bound = n * 2.0 ** -23 * float(np.abs(w.astype(np.float64) * x).sum())
+        vec = orc.dot_f16_f32(w, x)
+        orc.lib().wrs_oracle_force_scalar(1)
+        try:
+            sca = orc.dot_f16_f32(w, x)
+        finally:
+            orc.lib().wrs_oracle_force_scalar(0)
+        assert abs(vec - exact) <= bound and abs(sca - exact) <= bound
+
+
+def test_f16_linear_against_f64_layout_and_bias(orc):
+    rows, cols, T = 96, 320, 7
+    rng = np.random.default_rng(9)
+    w = (0.05 * rng.standard_normal((rows, cols))).astype(np.float16)
+    x = rng.standard_normal((T, cols)).astype(np.float32)
+    b = rng.standard_normal(rows).astype(np.float32)
+    out = np.full(T * rows, np.nan, np.float32)
+    orc.f16_linear(w, rows, cols, x.ravel(), b, T, out)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b  # [T][rows] = output[t*rows + r]
+    absw = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    assert (np.abs(out.reshape(T, rows) - ref) <= cols * 2.0 ** -23 * absw + 1e-6).all()
+    # no bias: the plain dot (quant.rs:464-467)
+    out2 = np.zeros(T * rows, np.float32)
+    orc.f16_linear(w, rows, cols, x.ravel(), None, T, out2)
+    assert np.array_equal(out2.reshape(T, rows) + b, out.reshape(T, rows))  # fl(dot + b)
+
+
+def test_f16_linear_identity_and_single_token(orc):
+    """W = I copies x exactly; the single-token branch (quant.rs:434-437) gives
+    the same numbers as one row of the multi-token branch."""
+    n = 64
+    x = np.random.default_rng(3).standard_normal((3, n)).astype(np.float32)
+    out = np.zeros(3 * n, np.float32)
+    orc.f16_linear(np.eye(n, dtype=np.float16), n, n, x.ravel(), None, 3, out)
+    assert np.array_equal(out, x.ravel())
+    w = np.random.default_rng(4).standard_normal((40, n)).astype(np.float16)
+    many = np.zeros(3 * 40, np.float32)
+    orc.f16_linear(w, 40, n, x.ravel(), None, 3, many)
+    one = np.zeros(40, np.float32)
+    orc.f16_linear(w, 40, n, x[1].copy(), None, 1, one)
+    assert np.array_equal(one, many.reshape(3, 40)[1])
+
+
+def test_f16_linear_asserts(orc):
+    w = np.zeros((4, 8), np.float16)
+    with pytest.raises(AssertionError):
+        orc.f16_linear(w, 4, 8, np.zeros(15, np.float32), None, 2, np.zeros(8, np.float32))

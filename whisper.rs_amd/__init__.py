@@ -34,7 +34,7 @@ KV_TILE = 128  # crates/tensor/src/ops/attention.rs:26
 __all__ = [
     "Context", "KvArena", "ExtensionMissing", "Layout", "flash_attention_2",
     "multi_head_attention", "single_token_mha_d64", "mha_with_cache", "prefill",
-    "token_major", "default_context", "header_symbols", "Q_TILE", "KV_TILE",
+    "token_major", "default_context", "header_symbols", "Q_TILE", "KV_TILE", "linear",
 ]
 
 
@@ -181,6 +181,35 @@ def prefill(q, k, v, out, *, batch, n_heads, t_q, t_kv, d_head, q_layout, kv_lay
         q_pos_offset), "wrs_attn_prefill")
 
 
+def linear(x, w, bias, out, *, out_row_stride=None, out_head_stride=64, ctx=None):
+    """LinearWeight::linear with f16 weights (crates/tensor/src/weight.rs:116-137,
+    crates/tensor/src/ops/quant.rs:415-473): out(t, r) = w[r] . x[t] + bias[r].
+
+    ``x`` [n_tokens][n_in] float32 or float16, ``w`` [n_out][n_in] float16,
+    ``bias`` float32 [n_out] or None, all CUDA tensors. ``out`` (float32,
+    float16 or bfloat16) receives out(t, r) at
+    t*out_row_stride + (r // 64)*out_head_stride + r % 64 elements from its start;
+    the defaults give token-major [n_tokens][n_out] rows.
+    """
+    ctx = ctx or default_context()
+    n_tokens, n_in = x.shape[0], x.shape[-1]
+    n_out = w.shape[0]
+    assert w.shape[1] == n_in and str(w.dtype) == "torch.float16"  # quant.rs:440
+    if bias is not None:
+        assert bias.numel() == n_out and str(bias.dtype) == "torch.float32"  # quant.rs:427
+    rs = n_out if out_row_stride is None else out_row_stride
+    ctx.check(_L.lib().wrs_linear(ctx.handle, _dtype_code(x), x.data_ptr(), _span(x),
+                                  x.stride(0) if x.dim() > 1 else n_in, w.data_ptr(),
+                                  None if bias is None else bias.data_ptr(), n_tokens, n_in,
+                                  n_out, _dtype_code(out), out.data_ptr(), _span(out), rs,
+                                  out_head_stride), "linear")
+
+
+def _span(t) -> int:
+    """Elements addressable from t.data_ptr() to the end of t's storage."""
+    return t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+
+
 class KvArena:
     """Device KV cache (``wrs_kv``), methods named after DecoderKvCache."""
 
@@ -303,6 +332,22 @@ class KvArena:
         self._c(self._lib.wrs_attn_prefill_cross(self.ctx.handle, self.handle, layer,
                                                  q.data_ptr(), q.shape[0], out.data_ptr()),
                 "prefill_cross")
+
+    def set_cross_proj(self, enc, w_k, w_v, b_v=None):
+        """precompute_cross_attn (crates/whisper/src/decoder.rs:423-447) into the
+        arena: per layer K = enc w_k^T, V = enc w_v^T + b_v, stored as f16
+        planes. ``enc`` [n_audio][d_model] float32/float16, ``w_k``/``w_v``
+        lists of [d_model][d_model] float16 tensors, ``b_v`` list of float32."""
+        n = len(w_k)
+        assert n == len(w_v) and (b_v is None or len(b_v) == n)
+        arr = ctypes.c_void_p * max(n, 1)
+        wk = arr(*[t.data_ptr() for t in w_k])
+        wv = arr(*[t.data_ptr() for t in w_v])
+        bv = None if b_v is None else arr(*[0 if t is None else t.data_ptr() for t in b_v])
+        self._c(self._lib.wrs_kv_set_cross_proj(self.handle, _dtype_code(enc), enc.data_ptr(),
+                                                _span(enc), enc.stride(0), enc.shape[0], wk,
+                                                wv, bv),
+                "set_cross_proj")
 
     def capture_cross_heads(self, layer, q, selected, n_selected, row_offset, out):
         """capture_cross_attention_heads (crates/whisper/src/decoder.rs:796-828).

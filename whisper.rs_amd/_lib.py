@@ -76,6 +76,11 @@ _SIGNATURES = {
     "wrs_attn_decode_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_self": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "wrs_linear": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _vp, _vp, _sz, _sz, _sz, _int,
+                          _vp, _sz, ctypes.c_int64, ctypes.c_int64]),
+    "wrs_kv_set_cross_proj": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _sz,
+                                     ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                     ctypes.POINTER(_vp)]),
     "wrs_attn_capture_cross_heads": (_int, [_vp, _vp, _sz, _vp, _sz, _szp, _szp, _sz, _sz, _sz,
                                             _vp, _sz]),
 }

@@ -32,6 +32,8 @@ struct wrs_attn_ctx {
   size_t counter_bytes = 0;
   float* cap_part = nullptr;  // alignment-head capture chunk statistics
   size_t cap_part_bytes = 0;
+  void* lin_x = nullptr;  // projections: split f16 rows of f32 activations + row scales
+  size_t lin_x_bytes = 0;
 };
 
 struct wrs_kv {
@@ -313,6 +315,7 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
   if (c->part) (void)hipFree(c->part);
   if (c->counters) (void)hipFree(c->counters);
   if (c->cap_part) (void)hipFree(c->cap_part);
+  if (c->lin_x) (void)hipFree(c->lin_x);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -870,6 +873,144 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, cons
     }
     WRS_HIP(c, wrs::launch_capture_cross_f16(a, c->stream));
   }
+  return WRS_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared front half of the projection entry points: validates x and the
+// shape, splits f32 rows into the context scratch, and fills the x part of
+// the launch arguments. Caller holds c->mu and the device guard.
+int linear_prepare(wrs_attn_ctx* c, int x_dtype, const void* x, int64_t x_rs, size_t n_tokens,
+                   size_t n_in, size_t n_out, wrs::LinearArgs& a) {
+  if (n_in == 0 || n_in % wrs::kLinearK != 0)
+    return fail(c, WRS_EUNSUPPORTED, "n_in must be a positive multiple of 64");
+  if (n_out % 4 != 0) return fail(c, WRS_EUNSUPPORTED, "n_out must be a multiple of 4");
+  if (n_tokens > static_cast<size_t>(INT32_MAX / 2) || n_in > (1u << 20) ||
+      n_out > static_cast<size_t>(INT32_MAX / 2))
+    return fail(c, WRS_EINVAL, "projection shape too large");
+  if (x_rs < static_cast<int64_t>(n_in)) return fail(c, WRS_EINVAL, "x row stride < n_in");
+  a.n_tokens = static_cast<int>(n_tokens);
+  a.n_in = static_cast<int>(n_in);
+  a.n_out = static_cast<int>(n_out);
+  if (x_dtype == WRS_F16) {
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (x_rs % 8))
+      return fail(c, WRS_EUNSUPPORTED, "f16 x rows must be 16-byte aligned");
+    a.x = static_cast<const _Float16*>(x);
+    a.x_rs = x_rs;
+    a.row_scale = nullptr;
+    a.k_total = a.n_in;
+    return WRS_OK;
+  }
+  if (x_dtype != WRS_F32) return fail(c, WRS_EUNSUPPORTED, "x must be f32 or f16");
+  const size_t split_bytes = align_up(n_tokens * 3 * n_in * 2, 256);
+  int rc = grow(c, &c->lin_x, &c->lin_x_bytes, split_bytes + n_tokens * 4, false);
+  if (rc) return rc;
+  auto* xs = static_cast<_Float16*>(c->lin_x);
+  auto* scale = reinterpret_cast<float*>(static_cast<char*>(c->lin_x) + split_bytes);
+  WRS_HIP(c, wrs::launch_linear_split(static_cast<const float*>(x), x_rs, a.n_tokens, a.n_in, xs,
+                                      scale, c->stream));
+  a.x = xs;
+  a.x_rs = 3 * static_cast<int64_t>(n_in);
+  a.row_scale = scale;
+  a.k_total = 3 * a.n_in;
+  return WRS_OK;
+}
+
+bool aligned_out(const void* p, int dt, int64_t rs, int64_t hs) {
+  const uintptr_t need = dt == WRS_F32 ? 16 : 8;
+  return (reinterpret_cast<uintptr_t>(p) % need) == 0 && rs % 4 == 0 && hs % 4 == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_t x_row_stride,
+               const void* w, const float* bias, size_t n_tokens, size_t n_in, size_t n_out,
+               int out_dtype, void* out, size_t out_len, int64_t out_row_stride,
+               int64_t out_head_stride) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (n_tokens == 0 || n_out == 0) return WRS_OK;  // quant.rs:430-432
+  if (!x || !w || !out) return fail(c, WRS_EINVAL, "null argument");
+  // quant.rs:424-425: x holds num_tokens rows of cols, output num_tokens * rows
+  if (x_row_stride < 0 || out_row_stride < 0 || out_head_stride < 0)
+    return fail(c, WRS_EINVAL, "negative stride");
+  if (x_len < (n_tokens - 1) * static_cast<size_t>(x_row_stride) + n_in)
+    return fail(c, WRS_EINVAL, "x shorter than n_tokens rows of n_in");
+  const size_t last_g = (n_out - 1) / 64;
+  const size_t max_off =
+      (n_tokens - 1) * static_cast<size_t>(out_row_stride) +
+      std::max(last_g * static_cast<size_t>(out_head_stride) + (n_out - 1) % 64,
+               last_g ? (last_g - 1) * static_cast<size_t>(out_head_stride) + 63 : 0);
+  if (out_len <= max_off) return fail(c, WRS_EINVAL, "out shorter than the written range");
+  if (out_dtype != WRS_F32 && out_dtype != WRS_F16 && out_dtype != WRS_BF16)
+    return fail(c, WRS_EINVAL, "unknown output dtype");
+  if (!aligned_out(out, out_dtype, out_row_stride, out_head_stride) ||
+      (reinterpret_cast<uintptr_t>(w) & 15) || (bias && (reinterpret_cast<uintptr_t>(bias) & 15)))
+    return fail(c, WRS_EUNSUPPORTED, "w/bias need 16-byte, out 4-element alignment");
+  DeviceGuard g(c->device);
+  wrs::LinearArgs a{};
+  int rc = linear_prepare(c, x_dtype, x, x_row_stride, n_tokens, n_in, n_out, a);
+  if (rc) return rc;
+  a.n_groups = 1;
+  a.out_rs = out_row_stride;
+  a.out_hs = out_head_stride;
+  a.w[0] = static_cast<const _Float16*>(w);
+  a.bias[0] = bias;
+  a.out[0] = out;
+  WRS_HIP(c, wrs::launch_linear_f16w(a, static_cast<wrs::DType>(out_dtype), c->stream));
+  return WRS_OK;
+}
+
+int wrs_kv_set_cross_proj(wrs_kv* kv, int x_dtype, const void* enc, size_t enc_len,
+                          int64_t enc_row_stride, size_t n_audio, const void* const* w_k,
+                          const void* const* w_v, const float* const* b_v) {
+  if (!kv) return WRS_EINVAL;
+  wrs_attn_ctx* c = kv->ctx;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (n_audio > kv->n_audio_max) return fail(c, WRS_ERANGE, "n_audio exceeds the arena");
+  if (!w_k || !w_v) return fail(c, WRS_EINVAL, "null weight arrays");
+  for (size_t l = 0; l < kv->n_layers; ++l) {
+    if (!w_k[l] || !w_v[l]) return fail(c, WRS_EINVAL, "null layer weight");
+    if ((reinterpret_cast<uintptr_t>(w_k[l]) & 15) || (reinterpret_cast<uintptr_t>(w_v[l]) & 15) ||
+        (b_v && b_v[l] && (reinterpret_cast<uintptr_t>(b_v[l]) & 15)))
+      return fail(c, WRS_EUNSUPPORTED, "weights and biases need 16-byte alignment");
+  }
+  if (n_audio > 0) {
+    if (!enc) return fail(c, WRS_EINVAL, "null encoder output");
+    if (enc_row_stride < 0 ||
+        enc_len < (n_audio - 1) * static_cast<size_t>(enc_row_stride) + kv->d_model())
+      return fail(c, WRS_EINVAL, "encoder output shorter than n_audio rows of d_model");
+    DeviceGuard g(c->device);
+    wrs::LinearArgs a{};
+    const size_t dm = kv->d_model();
+    int rc = linear_prepare(c, x_dtype, enc, enc_row_stride, n_audio, dm, dm, a);
+    if (rc) return rc;
+    a.out_rs = 64;  // [head][n_audio_max][64] planes
+    a.out_hs = static_cast<int64_t>(kv->n_audio_max * 64);
+    // decoder.rs:433-442: K without bias, V with cross_attn_v_b; every layer's
+    // K and V in as few launches as the group limit allows.
+    const size_t per_launch = wrs::kMaxLinearGroups / 2;
+    for (size_t l0 = 0; l0 < kv->n_layers; l0 += per_launch) {
+      const size_t nl = std::min(per_launch, kv->n_layers - l0);
+      a.n_groups = static_cast<int>(2 * nl);
+      for (size_t i = 0; i < nl; ++i) {
+        const size_t l = l0 + i;
+        a.w[2 * i] = static_cast<const _Float16*>(w_k[l]);
+        a.bias[2 * i] = nullptr;
+        a.out[2 * i] = reinterpret_cast<_Float16*>(kv->k_cross) + kv->cross_off(l);
+        a.w[2 * i + 1] = static_cast<const _Float16*>(w_v[l]);
+        a.bias[2 * i + 1] = b_v ? b_v[l] : nullptr;
+        a.out[2 * i + 1] = reinterpret_cast<_Float16*>(kv->v_cross) + kv->cross_off(l);
+      }
+      WRS_HIP(c, wrs::launch_linear_f16w(a, wrs::kF16, c->stream));
+    }
+  }
+  for (size_t l = 0; l < kv->n_layers; ++l) kv->cross_len[l] = n_audio;
   return WRS_OK;
 }
 

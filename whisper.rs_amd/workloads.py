@@ -168,6 +168,30 @@ class AlignmentCapture:
         return normal((self.n_audio, self.d_model), 3000 + layer, storage="f16")
 
 
+@dataclass(frozen=True)
+class Projection:
+    """LinearWeight::linear with f16 weights over a batch of token rows."""
+
+    name: str
+    n_tokens: int
+    n_in: int
+    n_out: int
+    x_storage: str  # f32 | f16
+
+    def flops(self) -> float:
+        return 2.0 * self.n_tokens * self.n_in * self.n_out
+
+    def x(self) -> np.ndarray:
+        return normal((self.n_tokens, self.n_in), 600, storage=self.x_storage)
+
+    def w(self) -> np.ndarray:
+        return normal((self.n_out, self.n_in), 601, sigma=self.n_in ** -0.5,
+                      storage="f16").astype(np.float16)
+
+    def bias(self) -> np.ndarray:
+        return normal((self.n_out,), 602, sigma=0.1)
+
+
 # crates/whisper/src/dtw.rs AlignmentHeadsPreset::LargeV3
 LARGE_V3_ALIGNMENT_HEADS = ((7, 0), (10, 17), (12, 18), (13, 12), (16, 1), (17, 14), (19, 11),
                             (21, 4), (24, 1), (25, 6))
@@ -184,3 +208,8 @@ SELF_DECODE_SWEEP = (32, 64, 128, 224, 256, 384, 448)
 # 124 text tokens + SOT, language, NOT and EOT (transcribe.rs:1403-1411)
 LARGE_DTW_CAPTURE = AlignmentCapture("whisper-large-v3 DTW alignment-head capture, 128 tokens",
                                      128, 20, 1500, 32, LARGE_V3_ALIGNMENT_HEADS)
+# encoder.rs:275-277 for 16 windows of 1500 frames (one layer), bf16 Q/K/V out
+LARGE_QKV_F16 = Projection("whisper-large-v3 encoder fused QKV projection x16 windows, f16 x",
+                           16 * 1500, 1280, 3840, "f16")
+LARGE_QKV_F32 = Projection("whisper-large-v3 encoder fused QKV projection x16 windows, f32 x",
+                           16 * 1500, 1280, 3840, "f32")
