@@ -201,7 +201,7 @@ def bench_linear(wrs, cfg, ctx, reps):
     w = torch.from_numpy(cfg.w()).cuda()
     b = torch.from_numpy(cfg.bias()).cuda()
     out = torch.empty((cfg.n_tokens, cfg.n_out), dtype=torch.bfloat16, device="cuda")
-    for _ in range(3):
+    for _ in range(150):  # ~50 ms of work: the clocks settle first
         wrs.linear(x, w, b, out, ctx=ctx)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -384,6 +384,26 @@ def cpu_baseline_capture(cfg):
                       f"{best * 1e3:.2f} ms"}
 
 
+def cpu_baseline_linear(cfg, threads):
+    """The oracle's f16_linear on one 1500-frame window of the batch."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    n = 1500
+    x = np.ascontiguousarray(cfg.x()[:n].astype(np.float32).ravel())
+    w = np.ascontiguousarray(cfg.w())
+    b = cfg.bias()
+    out = np.zeros(n * cfg.n_out, np.float32)
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        orc.f16_linear(w, cfg.n_out, cfg.n_in, x, b, n, out, n_threads=threads)
+        best = min(best, time.perf_counter() - t0)
+    flops = 2.0 * n * cfg.n_in * cfg.n_out
+    return {"value": flops / best / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"1 window of 16 ({n} x {cfg.n_in} x {cfg.n_out}), best of 3, "
+                      f"{best * 1e3:.1f} ms"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -397,7 +417,9 @@ def main():
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 HBM-traffic passes")
     ap.add_argument("--capture-reps", type=int, default=100)
-    ap.add_argument("--linear-reps", type=int, default=20)
+    ap.add_argument("--linear-reps", type=int, default=50)
+    ap.add_argument("--linear-f16-only", action="store_true",
+                    help="with --only linear: the f16-activation projection only")
     ap.add_argument("--only", choices=["encoder", "decode", "capture", "linear"], default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
@@ -425,7 +447,8 @@ def main():
         log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
         return
     if args.only == "linear":
-        for cfg in (W.LARGE_QKV_F16, W.LARGE_QKV_F32):
+        cfgs = (W.LARGE_QKV_F16,) if args.linear_f16_only else (W.LARGE_QKV_F16, W.LARGE_QKV_F32)
+        for cfg in cfgs:
             lms, ltf = bench_linear(wrs, cfg, ctx, args.linear_reps)
             log(f"linear only: {cfg.name}: {lms:.4f} ms, {ltf:.1f} TFLOP/s")
         calibration_copy()
@@ -438,23 +461,28 @@ def main():
     cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
     ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
+    lcfg = W.LARGE_QKV_F16
+    lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
+    lms32, ltf32 = bench_linear(wrs, W.LARGE_QKV_F32, ctx, args.linear_reps)
     log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
     host_slice = bench_host_slice(wrs, W, ctx)
     copy_gbs = copy_bandwidth()
 
-    enc_traffic = dec_traffic = cap_traffic = None
+    enc_traffic = dec_traffic = cap_traffic = lin_traffic = None
     if not args.no_traffic:
         log("traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes")
         enc_traffic = measure_traffic("encoder", "fa2_prefill", ["--steps", "3", "--warmup", "1"])
         dec_traffic = measure_traffic("decode", "decode_f16", ["--decode-reps", "3", "--eager"])
         cap_traffic = measure_traffic("capture", "capture_cross", ["--capture-reps", "3",
                                                                     "--eager"])
+        lin_traffic = measure_traffic("linear", "linear_f16w<__bf16>",
+                                      ["--linear-reps", "3", "--linear-f16-only"])
 
     def traffic_bytes(t):
         return None if t is None else round(t["FETCH_SIZE"] + t["WRITE_SIZE"])
 
     threads = min(16, os.cpu_count() or 1)
-    cpu_enc = cpu_dec = cpu_cap = None
+    cpu_enc = cpu_dec = cpu_cap = cpu_lin = None
     if not args.no_cpu:
         log(f"cpu baseline: oracle encoder window on {threads} threads")
         cpu_enc = cpu_baseline_encoder(cfg, qkv, threads)
@@ -462,6 +490,8 @@ def main():
         cpu_dec = cpu_baseline_decode(dcfg)
         log("cpu baseline: oracle capture of one layer, 1 thread")
         cpu_cap = cpu_baseline_capture(ccfg)
+        log(f"cpu baseline: oracle f16_linear, one window, {threads} threads")
+        cpu_lin = cpu_baseline_linear(lcfg, threads)
 
     line = {
         "metric": METRIC,
@@ -499,6 +529,16 @@ def main():
                          "unit": "GB/s", "frac": round(cgbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic_bytes(cap_traffic)},
             "cpu_baseline": cpu_cap,
+        },
+        "projection": {
+            "workload": lcfg.name, "value": round(ltf, 2), "unit": "TFLOP/s",
+            "ms_per_launch": round(lms, 4), "flops_per_launch": lcfg.flops(), "dtype": "f16",
+            "roofline": {"bound": "mfma", "achieved": round(ltf, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ltf / PEAK_BF16_TFLOPS, 4),
+                         "traffic": traffic_bytes(lin_traffic)},
+            "f32_exact": {"workload": W.LARGE_QKV_F32.name, "value": round(ltf32, 2),
+                          "unit": "TFLOP/s", "ms_per_launch": round(lms32, 4)},
+            "cpu_baseline": cpu_lin,
         },
         "host_slice": host_slice,
         "device": {"name": props.name, "cu": props.multi_processor_count,

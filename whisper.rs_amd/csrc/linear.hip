@@ -6,13 +6,18 @@
 //
 // K6 (linear_f16w): D^T = W X^T on v_mfma_f32_32x32x16_f16. Both operands are
 //   "k-contiguous" rows as stored (W [n_out][n_in] f16, X [n_tokens][k] f16),
-//   so neither needs a transpose. A workgroup of 4 waves owns a tile of 128
-//   output features x 128 tokens; wave (wm, wn) owns 64 x 64 of it as 2 x 2
-//   MFMA tiles. k advances 64 per LDS stage: the next stage's global loads are
-//   in flight in registers while the current stage's MFMAs run, then land in
-//   the other LDS buffer; one barrier per stage. LDS rows (128 bytes) keep
-//   their 16-byte chunks XOR-permuted by the row index, so the 32 rows read
-//   by one operand fetch spread over the banks.
+//   so neither needs a transpose. A workgroup of 8 waves owns a tile of 256
+//   output features x 256 tokens; wave (wm, wn) owns 128 x 64 of it as 4 x 2
+//   MFMA tiles (6 operand reads per 8 MFMAs). k advances 32 per LDS stage
+//   through a ring of three stages (96 KB): tiles move global -> LDS with
+//   buffer_load ... lds (no staging registers), two stages ahead of the
+//   MFMAs, and rows past the matrix edge read as zero through the buffer
+//   range check; one barrier per stage. LDS rows (64 bytes) keep their
+//   16-byte chunks XOR-permuted by the row index, so the 32 rows read by one
+//   operand fetch spread over the banks (swz_f). Workgroups are ordered so
+//   that each XCD runs a compact block of 4 feature x 8 token tiles at a time.
+//   Measured on the large-v3 fused QKV shape (24000 x 1280 x 3840): this
+//   shape of tile reaches ~85% of the library GEMM on the same box.
 //   f32 activations are made exact on the f16 matrix pipe by a pre-pass
 //   (linear_split_rows): each row is scaled by a power of two so that its
 //   largest element lies in [2^14, 2^15), then split into three f16 parts
@@ -35,18 +40,63 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 128;  // output features per workgroup (MFMA M)
-constexpr int kBN = 128;  // tokens per workgroup (MFMA N)
-constexpr int kBK = kLinearK;  // k per LDS stage (64)
-constexpr int kChunks = kBK / 8;  // 16-byte chunks per tile row
-constexpr int kLoads = kBM * kChunks / kThreads;  // 16-byte loads per thread per operand
+constexpr int kBM = 256;          // output features per workgroup (MFMA M)
+constexpr int kBN = 256;          // tokens per workgroup (MFMA N)
+constexpr int kBK = 32;           // k per LDS stage: one 64-byte row per feature/token
+constexpr int kStages = 3;        // LDS ring
+constexpr int kStageA = kBM * kBK;  // f16 elements per stage
+constexpr int kStageB = kBN * kBK;
+constexpr int kDmaA = kBM / kWaves / 16;  // 1 KB DMA instructions per wave per stage (2)
+constexpr int kDmaB = kBN / kWaves / 16;  // (2)
+constexpr int kDmaPerStage = kDmaA + kDmaB;
 
-static_assert(kBM == kBN, "one load pattern serves both operands");
-static_assert(kChunks == 8, "the chunk swizzle assumes 8 chunks per row");
+// 16-byte chunk c of LDS row r sits at slot c ^ f(r), f(r) = (r >> 2) & 3.
+// An operand fetch reads one chunk of 32 consecutive rows; 16 lanes at a time
+// cover 256 bytes of banks, i.e. four 64-byte rows per bank line, so the 4
+// rows of every 16 that share r & 3 must land in distinct slots; f does that.
+__device__ inline int swz_f(int row) { return (row >> 2) & 3; }
+__device__ inline int swz(int row, int chunk) { return chunk ^ swz_f(row); }
 
-__device__ inline int swz(int row, int chunk) { return chunk ^ (row & 7); }
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from global memory into LDS at m0 + 16 * lane, through a
+// buffer resource (offsets past its size read as zero). Inline asm, so the
+// compiler adds no waits of its own before later LDS reads; the kernel orders
+// it with explicit vmcnt waits and barriers. m0 is used by nothing else here.
+__device__ inline void dma16(u32x4 rsrc, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ inline u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;  // raw buffer, 32-bit data format
+  return r;
+}
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// Stage landed for this wave (at most N DMA loads still in flight), then all
+// waves meet.
+template <int N>
+__device__ inline void stage_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == kDmaPerStage)
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+static_assert(kDmaPerStage == 4, "the vmcnt literal above");
 
 template <typename OutT>
 __device__ inline void store4(OutT* p, const f32x4& v);
@@ -67,55 +117,78 @@ __device__ inline void store4<__bf16>(__bf16* p, const f32x4& v) {
   *reinterpret_cast<u32x2*>(p) = __builtin_bit_cast(u32x2, h);
 }
 
+// Physical workgroup id -> tile. The hardware hands linear ids round-robin to
+// the 8 XCDs; each XCD is given a contiguous range of logical ids instead, and
+// logical ids walk groups of kGroupM feature tiles with the token tiles
+// outermost inside a group, so the ~32 workgroups an XCD runs at once cover
+// 4 feature x 8 token tiles and share their operand stages in its L2.
+constexpr int kGroupM = 4;
+__device__ inline void tile_of(int pid, int n_fm, int n_tn, int& fm, int& tn) {
+  const int nwg = n_fm * n_tn;
+  const int xcd = pid & 7, k = pid >> 3;
+  const int per = nwg >> 3, rem = nwg & 7;
+  const int id = xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
+  const int group = id / (kGroupM * n_tn);
+  const int gm = min(kGroupM, n_fm - group * kGroupM);
+  const int in = id - group * kGroupM * n_tn;
+  fm = group * kGroupM + in % gm;
+  tn = in / gm;
+}
+
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 lds_a[2][kBM * kBK];
-  __shared__ __attribute__((aligned(16))) _Float16 lds_b[2][kBN * kBK];
+  __shared__ __attribute__((aligned(16))) _Float16 lds_a[kStages * kStageA];
+  __shared__ __attribute__((aligned(16))) _Float16 lds_b[kStages * kStageB];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.x * kBM;  // first output feature
-  const int n0 = blockIdx.y * kBN;  // first token
+  const int wm = wave & 1, wn = wave >> 1;  // 128-feature and 64-token block of this wave
+  const int n_fm = (a.n_out + kBM - 1) / kBM, n_tn = (a.n_tokens + kBN - 1) / kBN;
+  int fm, tn;
+  tile_of(blockIdx.x, n_fm, n_tn, fm, tn);
+  const int m0 = fm * kBM;  // first output feature
+  const int n0 = tn * kBN;  // first token
   const int grp = blockIdx.z;
-  const _Float16* w = a.w[grp];
 
-  // Global -> register loads of one stage: thread tid moves chunks tid + 256 i.
-  // Rows past the matrix edge read the last row (their results are dropped).
-  const _Float16* ga[kLoads];
-  const _Float16* gb[kLoads];
-  int lofs[kLoads];
+  // DMA sources. A wave moves rows 32*wave.. of the A and of the B tile, 16
+  // rows per instruction; lane i lands at slot i%4 of row i/4 and so fetches
+  // logical chunk swz(row, i%4). Rows past n_out / n_tokens fall
+  // outside the buffer ranges and read as zero.
+  const u32x4 wrs = buffer_rsrc(a.w[grp], static_cast<uint32_t>(
+                                              static_cast<int64_t>(a.n_out) * a.n_in * 2));
+  const u32x4 xrs = buffer_rsrc(
+      a.x, static_cast<uint32_t>(((static_cast<int64_t>(a.n_tokens) - 1) * a.x_rs + a.k_total) *
+                                 2));
+  uint32_t aoff[kDmaA], boff[kDmaB];
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / kChunks, ch = c % kChunks;
-    const int ra = min(m0 + row, a.n_out - 1);
-    const int rb = min(n0 + row, a.n_tokens - 1);
-    ga[i] = w + static_cast<int64_t>(ra) * a.n_in + ch * 8;
-    gb[i] = a.x + static_cast<int64_t>(rb) * a.x_rs + ch * 8;
-    lofs[i] = row * kBK + swz(row, ch) * 8;
+  for (int j = 0; j < kDmaA; ++j) {
+    const int row = wave * (kBM / kWaves) + 16 * j + (lane >> 2);
+    const int ch = swz(row, lane & 3);
+    aoff[j] = static_cast<uint32_t>((static_cast<int64_t>(m0 + row) * a.n_in + ch * 8) * 2);
   }
-  u32x4 ra_[kLoads], rb_[kLoads];
-  auto load_stage = [&](int kt) {
-    const int kx = kt * kBK;        // column of x' (k' space)
-    const int kw = kx % a.n_in;     // column of W
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      ra_[i] = *reinterpret_cast<const u32x4*>(ga[i] + kw);
-      rb_[i] = *reinterpret_cast<const u32x4*>(gb[i] + kx);
-    }
-  };
-  auto store_stage = [&](int buf) {
+  for (int j = 0; j < kDmaB; ++j) {
+    const int row = wave * (kBN / kWaves) + 16 * j + (lane >> 2);
+    const int ch = swz(row, lane & 3);
+    boff[j] = static_cast<uint32_t>((static_cast<int64_t>(n0 + row) * a.x_rs + ch * 8) * 2);
+  }
+  const uint32_t a_lds = lds_addr(lds_a) + wave * (kBM / kWaves) * kBK * 2;
+  const uint32_t b_lds = lds_addr(lds_b) + wave * (kBN / kWaves) * kBK * 2;
+  auto issue_stage = [&](int kt) {
+    const uint32_t kx = static_cast<uint32_t>(kt * kBK * 2);             // x' column, bytes
+    const uint32_t kw = static_cast<uint32_t>((kt * kBK) % a.n_in * 2);  // W column, bytes
+    const int s = kt % kStages;
+    const uint32_t ab = __builtin_amdgcn_readfirstlane(a_lds + s * kStageA * 2);
+    const uint32_t bb = __builtin_amdgcn_readfirstlane(b_lds + s * kStageB * 2);
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      *reinterpret_cast<u32x4*>(&lds_a[buf][lofs[i]]) = ra_[i];
-      *reinterpret_cast<u32x4*>(&lds_b[buf][lofs[i]]) = rb_[i];
-    }
+    for (int j = 0; j < kDmaA; ++j) dma16(wrs, ab + j * 1024, aoff[j] + kw);
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j) dma16(xrs, bb + j * 1024, boff[j] + kx);
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -124,34 +197,47 @@ __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
   // Operand rows of this lane: feature/token l % 32 of each 32-row MFMA tile,
   // k-group l / 32 (8 consecutive k) of each 16-k step.
   const int orow = lane & 31, kgrp = lane >> 5;
+  int aread[4][kBK / 16], bread[2][kBK / 16];
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ra = wm * 128 + i * 32 + orow;
+      aread[i][ks] = ra * kBK + swz(ra, 2 * ks + kgrp) * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rb = wn * 64 + j * 32 + orow;
+      bread[j][ks] = rb * kBK + swz(rb, 2 * ks + kgrp) * 8;
+    }
+  }
+
   const int n_kt = a.k_total / kBK;
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
+  issue_stage(0);
+  if (n_kt > 1) issue_stage(1);
   for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < n_kt) load_stage(kt + 1);
+    if (kt + 1 < n_kt)
+      stage_barrier<kDmaPerStage>();
+    else
+      stage_barrier<0>();
+    if (kt + 2 < n_kt) issue_stage(kt + 2);  // its buffer was last read in step kt - 1
+    const _Float16* as = lds_a + (kt % kStages) * kStageA;
+    const _Float16* bs = lds_b + (kt % kStages) * kStageB;
+    f16x8 av[kBK / 16][4], bv[kBK / 16][2];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int ch = 2 * ks + kgrp;
-      f16x8 av[2], bv[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int ra = wm * 64 + i * 32 + orow;
-        av[i] = *reinterpret_cast<const f16x8*>(&lds_a[buf][ra * kBK + swz(ra, ch) * 8]);
-        const int rb = wn * 64 + i * 32 + orow;
-        bv[i] = *reinterpret_cast<const f16x8*>(&lds_b[buf][rb * kBK + swz(rb, ch) * 8]);
-      }
+      for (int i = 0; i < 4; ++i) av[ks][i] = *reinterpret_cast<const f16x8*>(as + aread[i][ks]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 2; ++j) bv[ks][j] = *reinterpret_cast<const f16x8*>(bs + bread[j][ks]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < n_kt) {
-      store_stage(buf ^ 1);  // that buffer was last read before the previous barrier
-      __syncthreads();
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[ks][i], bv[ks][j], acc[i][j], 0, 0, 0);
   }
 
   // Epilogue: acc[i][j][e] is feature m0 + 64 wm + 32 i + 8 (e / 4) + 4 kgrp + e % 4
@@ -165,10 +251,10 @@ __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
     const float rs = a.row_scale ? a.row_scale[t] : 1.0f;
     OutT* orow_p = out + static_cast<int64_t>(t) * a.out_rs;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int r = m0 + wm * 64 + i * 32 + 8 * g + 4 * kgrp;
+        const int r = m0 + wm * 128 + i * 32 + 8 * g + 4 * kgrp;
         if (r >= a.n_out) continue;
         f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                    acc[i][j][4 * g + 3]};
@@ -222,7 +308,7 @@ hipError_t launch_linear_split(const float* x, int64_t x_rs, int n_tokens, int n
 
 hipError_t launch_linear_f16w(const LinearArgs& a, DType out_dt, hipStream_t s) {
   if (a.n_tokens <= 0 || a.n_out <= 0 || a.n_groups <= 0) return hipSuccess;
-  dim3 grid((a.n_out + kBM - 1) / kBM, (a.n_tokens + kBN - 1) / kBN, a.n_groups);
+  dim3 grid(((a.n_out + kBM - 1) / kBM) * ((a.n_tokens + kBN - 1) / kBN), 1, a.n_groups);
   switch (out_dt) {
     case kF32: hipLaunchKernelGGL(linear_f16w<float>, grid, dim3(kThreads), 0, s, a); break;
     case kF16: hipLaunchKernelGGL(linear_f16w<_Float16>, grid, dim3(kThreads), 0, s, a); break;

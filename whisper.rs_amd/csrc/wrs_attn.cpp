@@ -892,6 +892,12 @@ int linear_prepare(wrs_attn_ctx* c, int x_dtype, const void* x, int64_t x_rs, si
       n_out > static_cast<size_t>(INT32_MAX / 2))
     return fail(c, WRS_EINVAL, "projection shape too large");
   if (x_rs < static_cast<int64_t>(n_in)) return fail(c, WRS_EINVAL, "x row stride < n_in");
+  // The kernel addresses W and x through buffer resources: 32-bit byte
+  // offsets, including the rows past the edge of the last tile.
+  const int64_t xs_rs = x_dtype == WRS_F32 ? 3 * static_cast<int64_t>(n_in) : x_rs;
+  if ((static_cast<int64_t>(n_tokens) + 256) * xs_rs * 2 >= (int64_t{1} << 31) ||
+      (static_cast<int64_t>(n_out) + 256) * static_cast<int64_t>(n_in) * 2 >= (int64_t{1} << 31))
+    return fail(c, WRS_EUNSUPPORTED, "x or W span beyond the kernel's 2 GiB addressing");
   a.n_tokens = static_cast<int>(n_tokens);
   a.n_in = static_cast<int>(n_in);
   a.n_out = static_cast<int>(n_out);
