@@ -475,7 +475,7 @@ def main():
         dec_traffic = measure_traffic("decode", "decode_f16", ["--decode-reps", "3", "--eager"])
         cap_traffic = measure_traffic("capture", "capture_cross", ["--capture-reps", "3",
                                                                     "--eager"])
-        lin_traffic = measure_traffic("linear", "linear_f16w<__bf16>",
+        lin_traffic = measure_traffic("linear", "linear_f16w",
                                       ["--linear-reps", "3", "--linear-f16-only"])
 
     def traffic_bytes(t):
