@@ -215,6 +215,98 @@ def bench_linear(wrs, cfg, ctx, reps):
     return ms, cfg.flops() / (ms * 1e-3) / 1e12
 
 
+def bench_weight_stream(wrs, W, ctx, reps):
+    """One decoder step's projections for 5 beams, replayed from a HIP graph:
+    every launch streams its f16 weights once (the decode-sized linear path)."""
+    import torch
+    cfg = W.LARGE_DECODE_WEIGHTS
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED)
+    mats = cfg.matrices()
+    shapes = sorted(set(mats))
+    weights = {}
+    for r, c in shapes:
+        n = sum(1 for m in mats if m == (r, c))
+        weights[(r, c)] = [(torch.randn((r, c), generator=gen, device="cuda") * c ** -0.5).half()
+                           for _ in range(n)]
+    xs = {c: torch.randn((cfg.beams, c), generator=gen, device="cuda") for _, c in shapes}
+    outs = {r: torch.empty((cfg.beams, r), device="cuda") for r, _ in shapes}
+    seq, used = [], {k: 0 for k in shapes}
+    for m in mats:
+        seq.append((xs[m[1]], weights[m][used[m]], outs[m[0]]))
+        used[m] += 1
+
+    def step():
+        for x, w, o in seq:
+            wrs.linear(x, w, None, o, ctx=ctx)
+
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.use_torch_stream()
+        step()
+    ctx.use_torch_stream()
+    for _ in range(5):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"weight stream: timing {reps} graph replays of {len(seq)} launches")
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    # the vocabulary projection alone (the largest single stream)
+    xv, wv, ov = seq[-1]
+    for _ in range(10):
+        wrs.linear(xv, wv, None, ov, ctx=ctx)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        wrs.linear(xv, wv, None, ov, ctx=ctx)
+    end.record()
+    torch.cuda.synchronize()
+    ms_vocab = start.elapsed_time(end) / reps
+    vocab_bytes = cfg.n_vocab * cfg.d_model * 2
+    return cfg, ms, cfg.weight_bytes() / (ms * 1e-3) / 1e9, ms_vocab, \
+        vocab_bytes / (ms_vocab * 1e-3) / 1e9
+
+
+def bench_rows(wrs, ctx, reps):
+    """LayerNorm over the large-v3 encoder rows of 16 windows (24000 x 1280 f32
+    in, bf16 out, encoder.rs:266-274) and GELU over their MLP activations
+    (24000 x 5120 f32 in place): HBM-bound, algorithmic bytes = one read and
+    one write."""
+    import torch
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED)
+    T, d = 24000, 1280
+    x = torch.randn((T, d), generator=gen, device="cuda")
+    g = torch.randn(d, generator=gen, device="cuda")
+    b = torch.randn(d, generator=gen, device="cuda")
+    y = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    h = torch.randn((T, 4 * d), generator=gen, device="cuda")
+    res = {}
+    for name, fn, nbytes in (("layer_norm", lambda: wrs.layer_norm(x, g, b, 1e-5, y, ctx=ctx),
+                              T * d * (4 + 2)),
+                             ("gelu", lambda: wrs.gelu_inplace(h, ctx=ctx), T * 4 * d * 8)):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 4), "GBps": round(gbs, 1), "bytes": nbytes,
+                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"rows: {name}: {ms:.4f} ms, {gbs:.1f} GB/s")
+    return res
+
+
 def bench_host_slice(wrs, W, ctx, reps=20):
     """The host-slice drop-in (flash_attention_2 on f32 host slices, PCIe both
     ways) against the same call on device-resident f32 tensors, whisper-tiny
@@ -420,7 +512,10 @@ def main():
     ap.add_argument("--linear-reps", type=int, default=50)
     ap.add_argument("--linear-f16-only", action="store_true",
                     help="with --only linear: the f16-activation projection only")
-    ap.add_argument("--only", choices=["encoder", "decode", "capture", "linear"], default=None,
+    ap.add_argument("--stream-reps", type=int, default=20)
+    ap.add_argument("--rows-reps", type=int, default=50)
+    ap.add_argument("--only", choices=["encoder", "decode", "capture", "linear", "stream", "rows"],
+                    default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -453,6 +548,16 @@ def main():
             log(f"linear only: {cfg.name}: {lms:.4f} ms, {ltf:.1f} TFLOP/s")
         calibration_copy()
         return
+    if args.only == "rows":
+        bench_rows(wrs, ctx, args.rows_reps)
+        calibration_copy()
+        return
+    if args.only == "stream":
+        _, sms, sgbs, vms, vgbs = bench_weight_stream(wrs, W, ctx, args.stream_reps)
+        calibration_copy()
+        log(f"stream only: step {sms:.3f} ms, {sgbs:.1f} GB/s; vocabulary {vms * 1e3:.1f} us, "
+            f"{vgbs:.1f} GB/s")
+        return
     if args.only == "capture":
         _, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps, use_graph=not args.eager)
         calibration_copy()
@@ -464,6 +569,8 @@ def main():
     lcfg = W.LARGE_QKV_F16
     lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
     lms32, ltf32 = bench_linear(wrs, W.LARGE_QKV_F32, ctx, args.linear_reps)
+    scfg, sms, sgbs, vms, vgbs = bench_weight_stream(wrs, W, ctx, args.stream_reps)
+    rows = bench_rows(wrs, ctx, args.rows_reps)
     log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
     host_slice = bench_host_slice(wrs, W, ctx)
     copy_gbs = copy_bandwidth()
@@ -540,6 +647,16 @@ def main():
                           "unit": "TFLOP/s", "ms_per_launch": round(lms32, 4)},
             "cpu_baseline": cpu_lin,
         },
+        "decoder_weight_stream": {
+            "workload": scfg.name, "value": round(sgbs, 1), "unit": "GB/s",
+            "ms_per_step": round(sms, 4), "launches_per_step": len(scfg.matrices()),
+            "weight_bytes_per_step": scfg.weight_bytes(), "dtype": "f16",
+            "roofline": {"bound": "hbm", "achieved": round(sgbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(sgbs / PEAK_HBM_GBS, 4), "traffic": None},
+            "vocabulary_projection": {"us": round(vms * 1e3, 2), "GBps": round(vgbs, 1),
+                                      "frac_hbm": round(vgbs / PEAK_HBM_GBS, 4)},
+        },
+        "row_kernels": rows,
         "host_slice": host_slice,
         "device": {"name": props.name, "cu": props.multi_processor_count,
                    "copy_GBps": round(copy_gbs, 1)},

@@ -205,11 +205,24 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, co
  * out_dtype at out + t*out_row_stride + (r/64)*out_head_stride + r%64:
  * out_head_stride = 64 gives the reference's token-major [t][n_out] rows
  * (encoder.rs:275-277's fused QKV output, read in place by wrs_attn_prefill).
- * All pointers are device pointers. n_in % 64 == 0, n_out % 4 == 0. */
+ * All pointers are device pointers. n_in % 64 == 0. Batches of up to 8 rows
+ * (the beams of a decode step, f16_gemv_parallel at quant.rs:392-413) run on
+ * the weight-stream kernel and take any n_out; larger ones need n_out % 4 == 0. */
 int wrs_linear(wrs_attn_ctx *ctx, int x_dtype, const void *x, size_t x_len,
                int64_t x_row_stride, const void *w, const float *bias, size_t n_tokens,
                size_t n_in, size_t n_out, int out_dtype, void *out, size_t out_len,
                int64_t out_row_stride, int64_t out_head_stride);
+
+/* pub fn layer_norm(input, gamma, beta, eps, num_tokens, d_model, output)
+ * -- crates/tensor/src/ops/norm.rs:116-143 (asserts :124-127), device f32 rows;
+ * the output may be rounded to f16 / bf16 for a following projection.
+ * d_model % 4 == 0. */
+int wrs_layer_norm(wrs_attn_ctx *ctx, const float *x, size_t x_len, const float *gamma,
+                   const float *beta, float eps, size_t n_tokens, size_t d_model, int out_dtype,
+                   void *out, size_t out_len);
+/* pub fn gelu_inplace(data) -- crates/tensor/src/ops/gelu.rs:11-23, tanh form,
+ * in place on device f32. */
+int wrs_gelu_inplace(wrs_attn_ctx *ctx, float *data, size_t n);
 
 /* WhisperDecoder::precompute_cross_attn (crates/whisper/src/decoder.rs:423-447)
  * straight into the arena: for every layer l, K = enc . w_k[l]^T and

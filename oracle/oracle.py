@@ -71,6 +71,12 @@ def lib() -> ctypes.CDLL:
         L.wrs_oracle_f16_linear.argtypes = [_u16p, _sz, _sz, _f32p, _f32p, _sz, _f32p,
                                             ctypes.c_int]
         L.wrs_oracle_f16_linear.restype = ctypes.c_int
+        L.wrs_oracle_layer_norm.argtypes = [_f32p, _f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]
+        L.wrs_oracle_layer_norm.restype = ctypes.c_int
+        L.wrs_oracle_gelu.argtypes = [ctypes.c_float]
+        L.wrs_oracle_gelu.restype = ctypes.c_float
+        L.wrs_oracle_gelu_inplace.argtypes = [_f32p, _sz]
+        L.wrs_oracle_gelu_inplace.restype = None
         L.wrs_oracle_xorshift_fill.argtypes = [ctypes.POINTER(ctypes.c_uint32), _f32p, _sz]
         L.wrs_oracle_xorshift_fill.restype = None
         L.wrs_oracle_uses_avx2.argtypes = []
@@ -206,6 +212,24 @@ def f16_linear(w, rows, cols, x, bias, num_tokens, output, n_threads=None):
                                      None if bias is None else _ptr(bias), num_tokens,
                                      _ptr(output), _threads(n_threads))
     _check(rc, "f16_linear")
+
+
+def layer_norm(x, gamma, beta, eps, num_tokens, d_model, out):
+    """crates/tensor/src/ops/norm.rs:116-143."""
+    assert x.size == num_tokens * d_model and out.size == num_tokens * d_model  # :124-125
+    assert gamma.size == d_model and beta.size == d_model  # :126-127
+    lib().wrs_oracle_layer_norm(_ptr(x), _ptr(gamma), _ptr(beta), eps, num_tokens, d_model,
+                                _ptr(out))
+
+
+def gelu(x: float) -> float:
+    """crates/tensor/src/ops/gelu.rs:6-9."""
+    return float(lib().wrs_oracle_gelu(x))
+
+
+def gelu_inplace(data: np.ndarray) -> None:
+    """crates/tensor/src/ops/gelu.rs:11-23."""
+    lib().wrs_oracle_gelu_inplace(_ptr(data), data.size)
 
 
 def uses_avx2() -> bool:

@@ -16,6 +16,8 @@
  *   crates/tensor/src/simd.rs:593-700    dot_f16_f32 (AVX2+F16C and scalar)
  *   crates/tensor/src/ops/quant.rs:343-473 f16_linear (LinearWeight::linear
  *                                        with f16 weights, weight.rs:116-137)
+ *   crates/tensor/src/ops/norm.rs:1-143  layer_norm (AVX2 and scalar rows)
+ *   crates/tensor/src/ops/gelu.rs:1-23   gelu_scalar, gelu_inplace
  *   crates/tensor/tests/test_flash_attention_tiled.rs:15-35 xorshift32 inputs
  *
  * What pins each function (checked in tests/test_oracle.py):
@@ -599,6 +601,92 @@ int wrs_oracle_f16_linear(const uint16_t *w, size_t rows, size_t cols, const flo
         }
     }
     return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* norm.rs:1-143 layer_norm, gelu.rs:1-23 gelu_inplace                       */
+/* ------------------------------------------------------------------------ */
+static void layer_norm_row_scalar(const float *in, const float *gamma, const float *beta,
+                                  float eps, size_t d, float *out) {
+    /* norm.rs:67-92 */
+    float sum = 0.0f;
+    for (size_t i = 0; i < d; ++i) sum += in[i];
+    float mean = sum / (float)d;
+    float sum_sq = 0.0f;
+    for (size_t i = 0; i < d; ++i) {
+        float diff = in[i] - mean;
+        sum_sq += diff * diff;
+    }
+    float variance = sum_sq / (float)d;
+    float inv_std = 1.0f / sqrtf(variance + eps);
+    for (size_t i = 0; i < d; ++i) out[i] = (in[i] - mean) * inv_std * gamma[i] + beta[i];
+}
+
+#if WRS_HAVE_X86
+__attribute__((target("avx2,fma"))) static void layer_norm_row_avx2(const float *in,
+                                                                   const float *gamma,
+                                                                   const float *beta, float eps,
+                                                                   size_t d, float *out) {
+    /* norm.rs:3-64: 8-wide sums, hsum, scalar tails; normalize with fma(norm, g, b) */
+    size_t n_blocks = d / 8;
+    __m256 acc_sum = _mm256_setzero_ps();
+    for (size_t i = 0; i < n_blocks; ++i) acc_sum = _mm256_add_ps(acc_sum, _mm256_loadu_ps(in + 8 * i));
+    float sum = hsum256(acc_sum);
+    for (size_t i = n_blocks * 8; i < d; ++i) sum += in[i];
+    float mean = sum / (float)d;
+    __m256 v_mean = _mm256_set1_ps(mean);
+    __m256 acc_var = _mm256_setzero_ps();
+    for (size_t i = 0; i < n_blocks; ++i) {
+        __m256 diff = _mm256_sub_ps(_mm256_loadu_ps(in + 8 * i), v_mean);
+        acc_var = _mm256_fmadd_ps(diff, diff, acc_var);
+    }
+    float sum_sq = hsum256(acc_var);
+    for (size_t i = n_blocks * 8; i < d; ++i) {
+        float diff = in[i] - mean;
+        sum_sq += diff * diff;
+    }
+    float variance = sum_sq / (float)d;
+    float inv_std = 1.0f / sqrtf(variance + eps);
+    __m256 v_inv_std = _mm256_set1_ps(inv_std);
+    for (size_t i = 0; i < n_blocks; ++i) {
+        __m256 diff = _mm256_sub_ps(_mm256_loadu_ps(in + 8 * i), v_mean);
+        __m256 norm = _mm256_mul_ps(diff, v_inv_std);
+        _mm256_storeu_ps(out + 8 * i, _mm256_fmadd_ps(norm, _mm256_loadu_ps(gamma + 8 * i),
+                                                      _mm256_loadu_ps(beta + 8 * i)));
+    }
+    for (size_t i = n_blocks * 8; i < d; ++i) out[i] = (in[i] - mean) * inv_std * gamma[i] + beta[i];
+}
+#endif
+
+int wrs_oracle_layer_norm(const float *in, const float *gamma, const float *beta, float eps,
+                          size_t num_tokens, size_t d_model, float *out) {
+    /* norm.rs:116-143: rows in parallel (no cross-row arithmetic) */
+#pragma omp parallel for schedule(static) if (num_tokens > 1)
+    for (long t = 0; t < (long)num_tokens; ++t) {
+        const float *ri = in + (size_t)t * d_model;
+        float *ro = out + (size_t)t * d_model;
+#if WRS_HAVE_X86
+        if (wrs_oracle_uses_avx2()) {
+            layer_norm_row_avx2(ri, gamma, beta, eps, d_model, ro);
+            continue;
+        }
+#endif
+        layer_norm_row_scalar(ri, gamma, beta, eps, d_model, ro);
+    }
+    return 0;
+}
+
+/* gelu.rs:3-9: 0.5 x (1 + tanh(sqrt(2/pi) x (1 + 0.044715 x^2))), evaluated in
+ * the same order of operations (Rust does not contract a*b+c into an FMA). */
+float wrs_oracle_gelu(float x) {
+    const float GELU_COEF_A = 0.044715f, SQRT_2_OVER_PI = 0.7978846f;
+    float inner = SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+void wrs_oracle_gelu_inplace(float *data, size_t n) {
+#pragma omp parallel for schedule(static) if (n >= 4096)
+    for (long i = 0; i < (long)n; ++i) data[i] = wrs_oracle_gelu(data[i]);
 }
 
 /* ------------------------------------------------------------------------ */

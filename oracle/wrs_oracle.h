@@ -71,6 +71,13 @@ float wrs_oracle_f16_to_f32(uint16_t h);
 int wrs_oracle_f16_linear(const uint16_t *w, size_t rows, size_t cols, const float *x,
                           const float *bias, size_t num_tokens, float *out, int n_threads);
 
+/* norm.rs:116-143 layer_norm (rows of d_model, gamma/beta of d_model). */
+int wrs_oracle_layer_norm(const float *in, const float *gamma, const float *beta, float eps,
+                          size_t num_tokens, size_t d_model, float *out);
+/* gelu.rs:3-23 (tanh form). */
+float wrs_oracle_gelu(float x);
+void wrs_oracle_gelu_inplace(float *data, size_t n);
+
 /* xorshift32 generator of crates/tensor/tests/test_flash_attention_tiled.rs:15-35.
  * Fills out[0..n) and advances *state. */
 void wrs_oracle_xorshift_fill(uint32_t *state, float *out, size_t n);

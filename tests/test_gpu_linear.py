@@ -71,6 +71,37 @@ def test_linear_f32_matches_oracle(wrs, orc, ctx, n_tokens, n_in, n_out, use_bia
     assert (np.abs(got - ref) <= 2 * bound).all()
 
 
+@pytest.mark.parametrize("n_tokens,n_in,n_out,x_dt,out_dt", [
+    (1, 1280, 1280, "f32", torch.float32), (5, 1280, 5120, "f32", torch.float32),
+    (8, 5120, 1280, "f32", torch.float32), (5, 1280, 51866, "f16", torch.float32),
+    (3, 2112, 130, "f32", torch.bfloat16), (7, 4160, 1001, "f16", torch.float16)])
+def test_decode_weight_stream(wrs, orc, ctx, n_tokens, n_in, n_out, x_dt, out_dt):
+    """Decode-sized batches (quant.rs:392-413 / :434-437) on the weight-stream
+    kernel: any n_out (the vocabulary is 51866), x chunks past 2048 columns."""
+    note(f"gemv T={n_tokens} K={n_in} N={n_out} x={x_dt} out={out_dt}")
+    rng = np.random.default_rng(n_in + n_out + n_tokens)
+    x = rng.standard_normal((n_tokens, n_in)).astype(np.float32)
+    if x_dt == "f16":
+        x = x.astype(np.float16).astype(np.float32)
+    w = _weights(n_out, n_in, n_out)
+    b = rng.standard_normal(n_out).astype(np.float32)
+    xd = dev(x) if x_dt == "f32" else torch.from_numpy(x).half().cuda()
+    out = torch.full((n_tokens, n_out), float("nan"), dtype=out_dt, device="cuda")
+    wrs.linear(xd, torch.from_numpy(w).cuda(), dev(b), out, ctx=ctx)
+    got = out.float().cpu().numpy().astype(np.float64)
+    ref = np.zeros(n_tokens * n_out, np.float32)
+    orc.f16_linear(w, n_out, n_in, x.ravel(), b, n_tokens, ref)
+    ref = ref.reshape(n_tokens, n_out)
+    if out_dt == torch.float32:
+        tol = 2 * (_gamma_bound(x, w) + 2.0 ** -23 * np.abs(b))
+        assert (np.abs(got - ref) <= tol).all()
+    else:
+        rt = torch.from_numpy(ref).to(out_dt).float().numpy().astype(np.float64)
+        tol = _rounded_tol(x, w, rt, "f16" if out_dt == torch.float16 else "bf16") + \
+            2.0 ** -22 * np.abs(b)
+        assert (np.abs(got - rt) <= tol).all()
+
+
 def test_linear_f32_row_scaling(wrs, orc, ctx):
     """Rows of very different magnitude (1e-30 .. 1e30, a zero row) stay exact:
     each row is scaled by a power of two before the f16 split."""

@@ -495,3 +495,71 @@ def test_f16_linear_asserts(orc):
     w = np.zeros((4, 8), np.float16)
     with pytest.raises(AssertionError):
         orc.f16_linear(w, 4, 8, np.zeros(15, np.float32), None, 2, np.zeros(8, np.float32))
+
+
+# ---- layer_norm (crates/tensor/src/ops/norm.rs) and gelu (crates/tensor/src/ops/gelu.rs) ----
+
+def _ln_f64(x, g, b, eps):
+    x = x.astype(np.float64)
+    m = x.mean(axis=-1, keepdims=True)
+    v = ((x - m) ** 2).mean(axis=-1, keepdims=True)
+    return (x - m) / np.sqrt(v + eps) * g + b
+
+
+@pytest.mark.parametrize("d", [1, 7, 64, 384, 1280, 1283])
+def test_layer_norm_against_f64(orc, d):
+    rng = np.random.default_rng(d)
+    T = 6
+    x = (3.0 * rng.standard_normal((T, d)) + 1.5).astype(np.float32)
+    g = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    out = np.zeros(T * d, np.float32)
+    orc.layer_norm(x.ravel(), g, b, 1e-5, T, d, out)
+    ref = _ln_f64(x, g, b, 1e-5)
+    assert np.abs(out.reshape(T, d) - ref).max() <= 2e-5 * max(1.0, np.abs(ref).max())
+    orc.lib().wrs_oracle_force_scalar(1)
+    try:
+        out2 = np.zeros(T * d, np.float32)
+        orc.layer_norm(x.ravel(), g, b, 1e-5, T, d, out2)
+    finally:
+        orc.lib().wrs_oracle_force_scalar(0)
+    assert np.abs(out2.reshape(T, d) - ref).max() <= 2e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_layer_norm_closed_forms(orc):
+    d = 256
+    g = np.random.default_rng(1).standard_normal(d).astype(np.float32)
+    b = np.random.default_rng(2).standard_normal(d).astype(np.float32)
+    # a constant row has zero variance: the output is beta exactly
+    x = np.full((1, d), 3.25, np.float32)
+    out = np.zeros(d, np.float32)
+    orc.layer_norm(x.ravel(), g, b, 1e-5, 1, d, out)
+    assert np.array_equal(out, b)
+    # gamma = 1, beta = 0: mean 0 and variance v / (v + eps) of the output
+    x = np.random.default_rng(3).standard_normal((4, d)).astype(np.float32)
+    out = np.zeros(4 * d, np.float32)
+    orc.layer_norm(x.ravel(), np.ones(d, np.float32), np.zeros(d, np.float32), 1e-5, 4, d, out)
+    o = out.reshape(4, d).astype(np.float64)
+    v = x.astype(np.float64).var(axis=1)
+    assert np.abs(o.mean(axis=1)).max() < 1e-6
+    assert np.abs(o.var(axis=1) - v / (v + 1e-5)).max() < 1e-5
+
+
+def test_layer_norm_asserts(orc):
+    with pytest.raises(AssertionError):
+        orc.layer_norm(np.zeros(10, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32),
+                       1e-5, 2, 4, np.zeros(8, np.float32))
+
+
+def test_gelu_against_f64_and_closed_forms(orc):
+    x = np.linspace(-12, 12, 20001).astype(np.float32)
+    y = x.copy()
+    orc.gelu_inplace(y)
+    xd = x.astype(np.float64)
+    ref = 0.5 * xd * (1 + np.tanh(0.7978846 * xd * (1 + 0.044715 * xd * xd)))
+    assert np.abs(y - ref).max() <= 4e-7 * np.maximum(1.0, np.abs(ref)).max()
+    assert orc.gelu(0.0) == 0.0
+    # tanh-form identity: gelu(x) - gelu(-x) = x
+    assert np.abs((y - y[::-1]) - x).max() <= 2e-6 * 12
+    # large |x|: identity and zero
+    assert orc.gelu(30.0) == 30.0 and orc.gelu(-30.0) == 0.0

@@ -35,6 +35,7 @@ __all__ = [
     "Context", "KvArena", "ExtensionMissing", "Layout", "flash_attention_2",
     "multi_head_attention", "single_token_mha_d64", "mha_with_cache", "prefill",
     "token_major", "default_context", "header_symbols", "Q_TILE", "KV_TILE", "linear",
+    "layer_norm", "gelu_inplace",
 ]
 
 
@@ -203,6 +204,25 @@ def linear(x, w, bias, out, *, out_row_stride=None, out_head_stride=64, ctx=None
                                   None if bias is None else bias.data_ptr(), n_tokens, n_in,
                                   n_out, _dtype_code(out), out.data_ptr(), _span(out), rs,
                                   out_head_stride), "linear")
+
+
+def layer_norm(x, gamma, beta, eps, out, ctx=None):
+    """layer_norm (crates/tensor/src/ops/norm.rs:116-143) over the rows of the
+    float32 CUDA tensor x ([num_tokens][d_model]); out float32/float16/bfloat16."""
+    ctx = ctx or default_context()
+    d = x.shape[-1]
+    n = x.numel() // d if d else 0
+    ctx.check(_L.lib().wrs_layer_norm(ctx.handle, x.data_ptr(), x.numel(), gamma.data_ptr(),
+                                      beta.data_ptr(), eps, n, d, _dtype_code(out),
+                                      out.data_ptr(), out.numel()), "layer_norm")
+
+
+def gelu_inplace(data, ctx=None):
+    """gelu_inplace (crates/tensor/src/ops/gelu.rs:11-23) on a float32 CUDA tensor."""
+    ctx = ctx or default_context()
+    assert str(data.dtype) == "torch.float32" and data.is_contiguous()
+    ctx.check(_L.lib().wrs_gelu_inplace(ctx.handle, data.data_ptr(), data.numel()),
+              "gelu_inplace")
 
 
 def _span(t) -> int:

@@ -31,6 +31,8 @@
 //   (out_hs = 64) or the arena's [head][token][64] planes.
 #include "wrs_internal.hpp"
 
+#include <algorithm>
+
 namespace wrs {
 namespace {
 
@@ -265,6 +267,169 @@ __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
   }
 }
 
+// K7 (gemv_f16w): decode-sized batches (n_tokens <= 8: the beams of one step)
+//   against f16 weights, f16_gemv_parallel semantics (quant.rs:343-413). The
+//   weight stream is the whole cost, so every 16-byte chunk of W is read once
+//   for all rows. One persistent workgroup of 8 waves per CU stages all of x
+//   in LDS once (f32; f16 x widened exactly; at most kGemvXFloats values),
+//   then its waves walk groups of 4 output features (1 when n_out <= 4096, so
+//   that a d x d matrix still spreads over ~n_out / 8 CUs) across the matrix: lane l
+//   multiplies W[r][k..k+8) for k = 8 l + 512 m by the staged x of every row
+//   with f32 FMAs (the products dot_f16_f32 forms). The 16-byte loads of the
+//   next 2048-column batch (or of the next group) are in flight while a batch
+//   is multiplied. The row count is a template parameter (1..8), so no FMA is
+//   issued for absent rows; the 64 lane partials reduce with DPP and two
+//   cross-row moves, and lane b stores row b.
+constexpr int kGemvWaves = 8;
+constexpr int kGemvChunk = 2048;                // W columns per load batch
+constexpr int kGemvSmallOut = 4096;             // one feature per wave up to this n_out
+constexpr int kGemvSteps = kGemvChunk / 512;    // 16-byte W loads per row and batch
+
+template <int CTRL>
+__device__ inline float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                0xF, 0xF, false));
+}
+// Sum over the 64 lanes: xor 1, xor 2 (quad perms), the mirror of each half row
+// of 8 and of each row of 16 (DPP), then the two cross-row moves.
+__device__ inline float wave_sum64(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+template <int NT, int kGemvRowsPerWave, typename XT, typename OutT>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) float xs[kGemvXFloats];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int grp = blockIdx.y;
+  const int n_in = a.n_in;
+  const _Float16* w = a.w[grp];
+
+  OutT* out = reinterpret_cast<OutT*>(a.out[grp]);
+  const float* bias = a.bias[grp];
+  const int n_groups4 = (a.n_out + kGemvRowsPerWave - 1) / kGemvRowsPerWave;
+  const int stride = gridDim.x * kGemvWaves;
+  // W loads of one 2048-column batch of one group of 4 features.
+  auto load_w = [&](int g4, int c0, uint4 (&wv)[kGemvRowsPerWave][kGemvSteps]) {
+#pragma unroll
+    for (int i = 0; i < kGemvRowsPerWave; ++i) {
+      const int r = min(g4 * kGemvRowsPerWave + i, a.n_out - 1);
+      const _Float16* wr = w + static_cast<int64_t>(r) * n_in + c0;
+#pragma unroll
+      for (int m = 0; m < kGemvSteps; ++m) {
+        const int k = 8 * lane + 512 * m;
+        if (c0 + k < n_in) wv[i][m] = *reinterpret_cast<const uint4*>(wr + k);
+      }
+    }
+  };
+  int g4 = blockIdx.x * kGemvWaves + wave;
+  uint4 wv[kGemvRowsPerWave][kGemvSteps];
+  if (g4 < n_groups4) load_w(g4, 0, wv);  // in flight while x is staged
+
+  // Stage x: row b at xs[b * n_in ..], 8 columns per thread and step, the
+  // 16-byte loads of 4 steps in flight before their stores.
+  {
+    const int n8 = NT * n_in / 8;
+    for (int e0 = tid; e0 < n8; e0 += 4 * 64 * kGemvWaves) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u * 64 * kGemvWaves;
+        if (e < n8) {
+          const int b = (8 * e) / n_in, k = 8 * e - b * n_in;
+          const XT* src = static_cast<const XT*>(a.x) + b * a.x_rs + k;
+          if constexpr (sizeof(XT) == 4) {
+            const float4 lo = *reinterpret_cast<const float4*>(src);
+            const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+            v[u][0] = lo.x; v[u][1] = lo.y; v[u][2] = lo.z; v[u][3] = lo.w;
+            v[u][4] = hi.x; v[u][5] = hi.y; v[u][6] = hi.z; v[u][7] = hi.w;
+          } else {
+            const f16x8 h = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(src));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[u][j] = static_cast<float>(h[j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u * 64 * kGemvWaves;
+        if (e < n8) {
+          *reinterpret_cast<float4*>(&xs[8 * e]) = float4{v[u][0], v[u][1], v[u][2], v[u][3]};
+          *reinterpret_cast<float4*>(&xs[8 * e + 4]) = float4{v[u][4], v[u][5], v[u][6], v[u][7]};
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  for (; g4 < n_groups4; g4 += stride) {
+    float acc[kGemvRowsPerWave][NT];
+#pragma unroll
+    for (int i = 0; i < kGemvRowsPerWave; ++i)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) acc[i][b] = 0.0f;
+    for (int c0 = 0; c0 < n_in; c0 += kGemvChunk) {
+      uint4 cur[kGemvRowsPerWave][kGemvSteps];
+#pragma unroll
+      for (int i = 0; i < kGemvRowsPerWave; ++i)
+#pragma unroll
+        for (int m = 0; m < kGemvSteps; ++m) cur[i][m] = wv[i][m];
+      // the next batch (or the next group's first) is in flight during this one
+      if (c0 + kGemvChunk < n_in)
+        load_w(g4, c0 + kGemvChunk, wv);
+      else if (g4 + stride < n_groups4)
+        load_w(g4 + stride, 0, wv);
+#pragma unroll
+      for (int m = 0; m < kGemvSteps; ++m) {
+        const int k = c0 + 8 * lane + 512 * m;
+        if (k >= n_in) break;
+        float xv[NT][8];
+#pragma unroll
+        for (int b = 0; b < NT; ++b) {
+          const float4 lo = *reinterpret_cast<const float4*>(&xs[b * n_in + k]);
+          const float4 hi = *reinterpret_cast<const float4*>(&xs[b * n_in + k + 4]);
+          xv[b][0] = lo.x; xv[b][1] = lo.y; xv[b][2] = lo.z; xv[b][3] = lo.w;
+          xv[b][4] = hi.x; xv[b][5] = hi.y; xv[b][6] = hi.z; xv[b][7] = hi.w;
+        }
+#pragma unroll
+        for (int i = 0; i < kGemvRowsPerWave; ++i) {
+          const f16x8 h = __builtin_bit_cast(f16x8, cur[i][m]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float wf = static_cast<float>(h[j]);
+#pragma unroll
+            for (int b = 0; b < NT; ++b) acc[i][b] = fmaf(wf, xv[b][j], acc[i][b]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kGemvRowsPerWave; ++i)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) acc[i][b] = wave_sum64(acc[i][b]);
+    if (lane < NT) {
+      const int r0 = g4 * kGemvRowsPerWave;
+#pragma unroll
+      for (int i = 0; i < kGemvRowsPerWave; ++i) {
+        const int r = r0 + i;
+        if (r >= a.n_out) break;
+        float v = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NT; ++b)
+          if (b == lane) v = acc[i][b];
+        if (bias) v += bias[r];
+        out[static_cast<int64_t>(lane) * a.out_rs + static_cast<int64_t>(r >> 6) * a.out_hs +
+            (r & 63)] = static_cast<OutT>(v);
+      }
+    }
+  }
+}
+
 // f32 rows -> [hi | mid | lo] f16 rows of 3 n_in, plus each row's 2^-shift.
 // One wave per row.
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
@@ -303,6 +468,60 @@ hipError_t launch_linear_split(const float* x, int64_t x_rs, int n_tokens, int n
   if (n_tokens <= 0) return hipSuccess;
   hipLaunchKernelGGL(linear_split_rows, dim3((n_tokens + 3) / 4), dim3(256), 0, s, x, x_rs,
                      n_tokens, n_in, xs, row_scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStream_t s) {
+  if (a.n_tokens <= 0 || a.n_out <= 0 || a.n_groups <= 0) return hipSuccess;
+  if (a.n_tokens > kGemvMaxRows) return hipErrorInvalidValue;
+  if (a.n_tokens * a.n_in > kGemvXFloats) return hipErrorInvalidValue;
+  int dev = 0, n_cu = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  // Up to kGemvSmallOut features: one feature per wave, so that the matrix
+  // spreads over ~n_out / 8 CUs; beyond it 4 features per wave share each
+  // staged x read.
+  const int rpw = a.n_out <= kGemvSmallOut ? 1 : 4;
+  const int groups = (a.n_out + rpw - 1) / rpw;
+  const int wgs = std::min(n_cu, (groups + kGemvWaves - 1) / kGemvWaves);
+  dim3 grid(std::max(wgs, 1), a.n_groups);
+  dim3 block(64 * kGemvWaves);
+#define WRS_GEMV_R(R, XT, OT)                                                           \
+  switch (a.n_tokens) {                                                                 \
+    case 1: hipLaunchKernelGGL((gemv_f16w<1, R, XT, OT>), grid, block, 0, s, a); break;  \
+    case 2: hipLaunchKernelGGL((gemv_f16w<2, R, XT, OT>), grid, block, 0, s, a); break;  \
+    case 3: hipLaunchKernelGGL((gemv_f16w<3, R, XT, OT>), grid, block, 0, s, a); break;  \
+    case 4: hipLaunchKernelGGL((gemv_f16w<4, R, XT, OT>), grid, block, 0, s, a); break;  \
+    case 5: hipLaunchKernelGGL((gemv_f16w<5, R, XT, OT>), grid, block, 0, s, a); break;  \
+    case 6: hipLaunchKernelGGL((gemv_f16w<6, R, XT, OT>), grid, block, 0, s, a); break;  \
+    case 7: hipLaunchKernelGGL((gemv_f16w<7, R, XT, OT>), grid, block, 0, s, a); break;  \
+    default: hipLaunchKernelGGL((gemv_f16w<8, R, XT, OT>), grid, block, 0, s, a); break; \
+  }
+#define WRS_GEMV(XT, OT)          \
+  if (rpw == 1) {                 \
+    WRS_GEMV_R(1, XT, OT)         \
+  } else {                        \
+    WRS_GEMV_R(4, XT, OT)         \
+  }
+  if (x_dt == kF32) {
+    switch (out_dt) {
+      case kF32: WRS_GEMV(float, float); break;
+      case kF16: WRS_GEMV(float, _Float16); break;
+      case kBF16: WRS_GEMV(float, __bf16); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else if (x_dt == kF16) {
+    switch (out_dt) {
+      case kF32: WRS_GEMV(_Float16, float); break;
+      case kF16: WRS_GEMV(_Float16, _Float16); break;
+      case kBF16: WRS_GEMV(_Float16, __bf16); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef WRS_GEMV
+#undef WRS_GEMV_R
   return hipGetLastError();
 }
 

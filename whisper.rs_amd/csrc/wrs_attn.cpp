@@ -955,10 +955,40 @@ int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_
   if (out_len <= max_off) return fail(c, WRS_EINVAL, "out shorter than the written range");
   if (out_dtype != WRS_F32 && out_dtype != WRS_F16 && out_dtype != WRS_BF16)
     return fail(c, WRS_EINVAL, "unknown output dtype");
-  if (!aligned_out(out, out_dtype, out_row_stride, out_head_stride) ||
-      (reinterpret_cast<uintptr_t>(w) & 15) || (bias && (reinterpret_cast<uintptr_t>(bias) & 15)))
-    return fail(c, WRS_EUNSUPPORTED, "w/bias need 16-byte, out 4-element alignment");
+  if (reinterpret_cast<uintptr_t>(w) & 15) return fail(c, WRS_EUNSUPPORTED, "w needs 16-byte alignment");
   DeviceGuard g(c->device);
+  if (n_tokens <= static_cast<size_t>(wrs::kGemvMaxRows) &&
+      n_tokens * n_in <= static_cast<size_t>(wrs::kGemvXFloats)) {
+    // Decode-sized batch: the f16 weight stream (f16_gemv_parallel, quant.rs:392-413);
+    // any n_out, element-wise stores.
+    if (n_in == 0 || n_in % wrs::kLinearK != 0)
+      return fail(c, WRS_EUNSUPPORTED, "n_in must be a positive multiple of 64");
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (x_row_stride % (x_dtype == WRS_F32 ? 4 : 8)))
+      return fail(c, WRS_EUNSUPPORTED, "x rows must be 16-byte aligned");
+    if (x_dtype != WRS_F32 && x_dtype != WRS_F16)
+      return fail(c, WRS_EUNSUPPORTED, "x must be f32 or f16");
+    if (x_row_stride < static_cast<int64_t>(n_in) || n_in > (1u << 24) ||
+        n_out > static_cast<size_t>(INT32_MAX / 2))
+      return fail(c, WRS_EINVAL, "projection shape");
+    wrs::GemvArgs gv{};
+    gv.x = x;
+    gv.x_rs = x_row_stride;
+    gv.n_tokens = static_cast<int>(n_tokens);
+    gv.n_in = static_cast<int>(n_in);
+    gv.n_out = static_cast<int>(n_out);
+    gv.n_groups = 1;
+    gv.out_rs = out_row_stride;
+    gv.out_hs = out_head_stride;
+    gv.w[0] = static_cast<const _Float16*>(w);
+    gv.bias[0] = bias;
+    gv.out[0] = out;
+    WRS_HIP(c, wrs::launch_gemv_f16w(gv, static_cast<wrs::DType>(x_dtype),
+                                     static_cast<wrs::DType>(out_dtype), c->stream));
+    return WRS_OK;
+  }
+  if (!aligned_out(out, out_dtype, out_row_stride, out_head_stride) ||
+      (bias && (reinterpret_cast<uintptr_t>(bias) & 15)))
+    return fail(c, WRS_EUNSUPPORTED, "bias needs 16-byte, out 4-element alignment");
   wrs::LinearArgs a{};
   int rc = linear_prepare(c, x_dtype, x, x_row_stride, n_tokens, n_in, n_out, a);
   if (rc) return rc;
@@ -969,6 +999,43 @@ int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_
   a.bias[0] = bias;
   a.out[0] = out;
   WRS_HIP(c, wrs::launch_linear_f16w(a, static_cast<wrs::DType>(out_dtype), c->stream));
+  return WRS_OK;
+}
+
+int wrs_layer_norm(wrs_attn_ctx* c, const float* x, size_t x_len, const float* gamma,
+                   const float* beta, float eps, size_t n_tokens, size_t d_model, int out_dtype,
+                   void* out, size_t out_len) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  // norm.rs:124-127
+  if (x_len != n_tokens * d_model || out_len != n_tokens * d_model)
+    return fail(c, WRS_EINVAL, "input/output length != num_tokens * d_model");
+  if (n_tokens == 0 || d_model == 0) return WRS_OK;
+  if (!x || !gamma || !beta || !out) return fail(c, WRS_EINVAL, "null argument");
+  if (out_dtype != WRS_F32 && out_dtype != WRS_F16 && out_dtype != WRS_BF16)
+    return fail(c, WRS_EINVAL, "unknown output dtype");
+  if (d_model % 4 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
+      (reinterpret_cast<uintptr_t>(gamma) & 15) || (reinterpret_cast<uintptr_t>(beta) & 15) ||
+      (reinterpret_cast<uintptr_t>(out) & (out_dtype == WRS_F32 ? 15 : 7)))
+    return fail(c, WRS_EUNSUPPORTED, "d_model % 4 and 16-byte aligned rows required");
+  if (n_tokens > static_cast<size_t>(INT32_MAX) || d_model > static_cast<size_t>(INT32_MAX / 4))
+    return fail(c, WRS_EINVAL, "layer_norm shape too large");
+  DeviceGuard g(c->device);
+  WRS_HIP(c, wrs::launch_layer_norm(x, gamma, beta, eps, static_cast<int>(n_tokens),
+                                    static_cast<int>(d_model),
+                                    static_cast<wrs::DType>(out_dtype), out, c->stream));
+  return WRS_OK;
+}
+
+int wrs_gelu_inplace(wrs_attn_ctx* c, float* data, size_t n) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (n == 0) return WRS_OK;
+  if (!data) return fail(c, WRS_EINVAL, "null argument");
+  if (reinterpret_cast<uintptr_t>(data) & 15)
+    return fail(c, WRS_EUNSUPPORTED, "data must be 16-byte aligned");
+  DeviceGuard g(c->device);
+  WRS_HIP(c, wrs::launch_gelu(data, static_cast<int64_t>(n), c->stream));
   return WRS_OK;
 }
 

@@ -126,9 +126,30 @@ struct LinearArgs {
   void* out[kMaxLinearGroups];
 };
 hipError_t launch_linear_f16w(const LinearArgs& a, DType out_dt, hipStream_t s);
+// Decode-sized batches (n_tokens <= kGemvMaxRows) of the same product on the
+// f16 weight stream; x is f32 or f16 with row stride x_rs, no split needed.
+constexpr int kGemvMaxRows = 8;
+constexpr int kGemvXFloats = 40960;  // n_tokens * n_in staged in LDS (160 KB)
+struct GemvArgs {
+  const void* x;
+  int64_t x_rs;
+  int n_tokens, n_in, n_out, n_groups;
+  int64_t out_rs, out_hs;
+  const _Float16* w[kMaxLinearGroups];
+  const float* bias[kMaxLinearGroups];
+  void* out[kMaxLinearGroups];
+};
+hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStream_t s);
 // f32 rows -> [hi | mid | lo] f16 rows (3 n_in each) and per-row 2^-shift.
 hipError_t launch_linear_split(const float* x, int64_t x_rs, int n_tokens, int n_in,
                                _Float16* xs, float* row_scale, hipStream_t s);
+
+// LayerNorm over f32 rows (norm.rs:116-143), output f32/f16/bf16 rows of d;
+// d % 4 == 0, rows 16-byte aligned.
+hipError_t launch_layer_norm(const float* x, const float* gamma, const float* beta, float eps,
+                             int n_tokens, int d, DType out_dt, void* out, hipStream_t s);
+// GELU, tanh form, in place on f32 (gelu.rs:11-23); data 16-byte aligned.
+hipError_t launch_gelu(float* data, int64_t n, hipStream_t s);
 
 // KV arena kernels.
 // f32 rows [n][d_model] (row stride src_rs) -> f16 planes: head h, row i at

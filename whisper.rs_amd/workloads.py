@@ -213,3 +213,29 @@ LARGE_QKV_F16 = Projection("whisper-large-v3 encoder fused QKV projection x16 wi
                            16 * 1500, 1280, 3840, "f16")
 LARGE_QKV_F32 = Projection("whisper-large-v3 encoder fused QKV projection x16 windows, f32 x",
                            16 * 1500, 1280, 3840, "f32")
+
+
+@dataclass(frozen=True)
+class DecoderWeightStream:
+    """The projections of one decoder step for `beams` rows: per layer
+    q, k, v, out, cross q, cross out (d x d), mlp0 (4d x d) and mlp2 (d x 4d)
+    (decoder.rs:596-760), then the vocabulary projection (decoder.rs:781-783)."""
+
+    name: str
+    beams: int
+    d_model: int
+    n_layers: int
+    n_vocab: int
+
+    def matrices(self) -> list[tuple[int, int]]:
+        d = self.d_model
+        per_layer = [(d, d)] * 6 + [(4 * d, d), (d, 4 * d)]
+        return per_layer * self.n_layers + [(self.n_vocab, d)]
+
+    def weight_bytes(self) -> int:
+        return sum(r * c * 2 for r, c in self.matrices())
+
+
+LARGE_DECODE_WEIGHTS = DecoderWeightStream(
+    "whisper-large-v3 decoder step projections, beam 5 (32 layers + vocabulary)", 5, 1280, 32,
+    51866)
