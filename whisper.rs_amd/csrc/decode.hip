@@ -3,15 +3,26 @@
 // K2 (decode_f16): split-K attention over the f16 KV cache
 //   (replaces crates/tensor/src/ops/attention.rs:246-434 single_token_mha_d64
 //    as called from crates/whisper/src/decoder.rs:636 / :698).
-//   Grid (split, head, group). A workgroup of 1024 threads owns kChunk = 128
+//   Grid (split, head, group). A workgroup of 8 waves owns kChunk = 128
 //   consecutive keys of one (group, head) plane and ALL query rows of the
 //   group (the beams of an utterance share the cross-attention plane, so it is
-//   read once per step instead of once per beam). Eight threads carry one key
-//   (16 bytes of its K row and of its V row each) and issue those loads, and
-//   the query loads, before any arithmetic, so the whole layer's cache is in
-//   flight from the first cycles. 16 waves per workgroup (4 per SIMD) keep the
-//   short score / softmax / PV phases from being bound by one wave's issue
-//   rate.
+//   read once per step instead of once per beam). Each wave takes 16 keys,
+//   and every lane issues its q loads and its four 16-byte K/V loads before
+//   any arithmetic, so the whole layer's cache is in flight from the first
+//   cycles. The arithmetic runs on the matrix pipe, in registers:
+//   - scores: one 16x16x32 f16 MFMA tile S^T = K Q^T per 32 d. The K rows
+//     are the A operand exactly as loaded (lane (c, g): key c, d 8g..8g+7).
+//     q*scale*log2(e) is scaled by a power of two per row and split into f16
+//     high and low parts, placed in B columns r and r+8; a row_ror-8 DPP adds
+//     the two columns, so the scores carry ~2^-22 relative error, not f16's.
+//   - softmax: the 16 keys' max and exp2 sum per row, over the lane's 4
+//     values and two cross-row moves.
+//   - P V: V^T comes out of a 16x16x32 MFMA of the V rows against a 0/1
+//     selection matrix (exact), already in the B layout of a 16x16x16 MFMA
+//     whose A operand is P as produced by the score tile, again as high
+//     (rows 0-7) and low (rows 8-15) f16 parts.
+//   The waves' (max, sum, 16x64 partials) meet in LDS; thread (row, d) folds
+//   them with the log-sum-exp rule.
 //   Partials (max, sum, acc[64]) per row are published with agent-scope
 //   (sc1, L2-coherent) stores; after every wave has waited for its stores, one
 //   thread bumps the (group, head) counter -- each on its own 128-byte line, so
@@ -34,28 +45,22 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;            // exact f32 decode
-constexpr int kWgThreads = 1024;         // f16 split-K decode: 16 waves, 4 per SIMD
-constexpr int kChunk = kDecodeChunk;     // keys per workgroup: one per 8 threads
-constexpr int kKeyGroups = kWgThreads / 64;  // PV: 16 groups of kChunk/16 keys
-constexpr int kKpl = kChunk / 64;        // softmax: keys per lane
+constexpr int kChunk = kDecodeChunk;     // keys per workgroup
+constexpr int kMWaves = kChunk / 16;     // one 16-key MFMA tile per wave
+constexpr int kRedPitch = 68;            // LDS pitch (floats) of a wave's 16 output rows
 constexpr int kPart = 68;    // floats per partial row: m, l, 2 pad, acc[64]
 constexpr int kCounterStride = 32;  // 128 bytes between merge counters
 constexpr int kMaxSplitsMerge = 16;  // partial loads in flight per thread in the merge
 
-// Cross-lane moves inside a row of 16 lanes (DPP): xor 1, xor 2, mirror-8, mirror-16.
+// Cross-lane moves inside a row of 16 lanes (DPP): xor 1, xor 2, mirror-8, mirror-16,
+// rotate by 8.
 template <int CTRL>
 __device__ inline float dpp(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
                                                                 0xF, 0xF, false));
-}
-// Sum over the 8 lanes 8i..8i+7: xor 1, xor 2 (quad perm), then row_half_mirror
-// (lane 7-j of each half row of 8) adds the other quad.
-__device__ inline float oct_sum(float x) {
-  x += dpp<0xB1>(x);
-  x += dpp<0x4E>(x);
-  return x + dpp<0x141>(x);
 }
 __device__ inline float wave_max(float x) {
   x = fmaxf(x, dpp<0xB1>(x));
@@ -81,127 +86,153 @@ __device__ inline float ld_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
+__device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
+
+static_assert(kMWaves >= kMaxRowsPerGroup, "one merging wave per query row");
+
 template <int R>
-__global__ __launch_bounds__(kWgThreads) void decode_f16(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) float qs[R][64];
-  __shared__ float ps[R][kChunk];
-  __shared__ __attribute__((aligned(16))) _Float16 vs[kChunk][64 + 8];
-  __shared__ float red[kKeyGroups][R][64];
-  __shared__ float mrow[R], lrow[R];
+__global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
+  __shared__ float red[kMWaves][16][kRedPitch];
+  __shared__ float wm[kMWaves][8], wl[kMWaves][8];
   __shared__ int last_flag;
 
   const int split = blockIdx.x, h = blockIdx.y, g = blockIdx.z;
-  const int tid = threadIdx.x;
-  const int rows = a.rows_per_group;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  constexpr int rows = R;  // == a.rows_per_group
   const int len = a.len[g];
-  // Loads: thread (key kl, eighth pt) carries d 8*pt..8*pt+7 of one K row and
-  // one V row of the chunk; threads below R*64 also carry one query element.
-  const int pt = tid & 7, kl = tid >> 3;
+  const int col = lane & 15, kg = lane >> 4;
+  const bool lo_part = col >= 8;
+
+  const int qrow = col & 7;
+  float qv[16];
+  {
+    const float* qp = a.q + static_cast<int64_t>(g * rows + (qrow < rows ? qrow : 0)) * a.q_rs + h * 64 + 8 * kg;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qv[j] = qp[j];
+      qv[8 + j] = qp[32 + j];
+    }
+  }
+  // Lane (col, kg) carries key kbase + col: d 8kg..8kg+7 and 32+8kg.. of its
+  // K and V rows (the A-operand layout of a 16x16x32 MFMA).
+  const int kbase = split * kChunk + wave * 16;
+  const bool valid = kbase + col < len;
+  const int64_t off = a.goff[g] + h * a.kv_hs + static_cast<int64_t>(valid ? kbase + col : 0) * 64 + 8 * kg;
+  const u32x4 kx0 = *reinterpret_cast<const u32x4*>(a.k + off);
+  const u32x4 kx1 = *reinterpret_cast<const u32x4*>(a.k + off + 32);
+  u32x4 vx0 = *reinterpret_cast<const u32x4*>(a.v + off);
+  u32x4 vx1 = *reinterpret_cast<const u32x4*>(a.v + off + 32);
+  // Every load above is issued before any of them is waited on: the q
+  // arithmetic below depends on a value defined after them.
+  float one;
+  __asm__ volatile("v_mov_b32 %0, 1.0" : "=v"(one) : : "memory");
+  const u32x4 zero4 = {0, 0, 0, 0};
+  vx0 = valid ? vx0 : zero4;
+  vx1 = valid ? vx1 : zero4;
+
+  // q * scale * log2(e), scaled by 2^sh so the row max lies in [2^14, 2^15),
+  // split into f16 high (columns 0-7 of B) and low (columns 8-15) parts.
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    qv[j] = (qrow < rows ? qv[j] : 0.f) * (a.scale_log2 * one);
+    amax = fmaxf(amax, fabsf(qv[j]));
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+  const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
+  const float up = pow2(sh), down = pow2(clamp_exp(-sh));
+  f16x8 b0, b1;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x0 = qv[j] * up, x1 = qv[8 + j] * up;
+    const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
+    b0[j] = lo_part ? static_cast<_Float16>(x0 - static_cast<float>(h0)) : h0;
+    b1[j] = lo_part ? static_cast<_Float16>(x1 - static_cast<float>(h1)) : h1;
+  }
+
+  // S^T tile: lane (col, kg) gets keys kbase+4kg+i of column col; the high and
+  // low columns of a row are eight lanes apart (row_ror 8 adds them).
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kx0), b0, s, 0, 0, 0);
+  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kx1), b1, s, 0, 0, 0);
+  float sc[4], mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float si = s[i];
+    const float full = (si + dpp<0x128>(si)) * down;
+    sc[i] = (kbase + 4 * kg + i < len) ? full : -INFINITY;
+    mx = fmaxf(mx, sc[i]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float sum = 0.f;
+  f16x4 pa;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float p = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc[i] - mx);
+    sum += p;
+    const _Float16 ph = static_cast<_Float16>(p);
+    pa[i] = lo_part ? static_cast<_Float16>(p - static_cast<float>(ph)) : ph;
+  }
+  sum += __shfl_xor(sum, 16);
+  sum += __shfl_xor(sum, 32);
+
+  // V^T by multiplying with a 0/1 selection matrix (exact), then P V.
+  f16x8 e0, e1;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    e0[j] = (8 * kg + j == col) ? static_cast<_Float16>(1.f) : static_cast<_Float16>(0.f);
+    e1[j] = (8 * kg + j == 16 + col) ? static_cast<_Float16>(1.f) : static_cast<_Float16>(0.f);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8, dt < 2 ? vx0 : vx1), (dt & 1) ? e1 : e0, z, 0, 0, 0);
+    const f16x4 vb = __builtin_convertvector(t, f16x4);
+    const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, z, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][4 * kg + i][16 * dt + col] = o[i];
+  }
+  if (kg == 0 && col < 8) {
+    wm[wave][col] = mx;
+    wl[wave][col] = sum;
+  }
+  __syncthreads();
+
+  // Thread (row qr, d qd) of the first rows*64 threads folds the waves'
+  // partials (log-sum-exp, exp2 domain); rows r and r+8 are the high and low
+  // parts of the weights.
   const int qr = tid >> 6, qd = tid & 63;
-  float qv = 0.f;
-  if (qr < rows)
-    qv = a.q[static_cast<int64_t>(g * rows + qr) * a.q_rs + h * 64 + qd];
-  const int key = split * kChunk + kl;
-  const bool valid = key < len;
-  u32x4 kx = {0, 0, 0, 0}, vx = {0, 0, 0, 0};
-  if (valid) {
-    const int64_t off = a.goff[g] + h * a.kv_hs + static_cast<int64_t>(key) * 64 + pt * 8;
-    kx = *reinterpret_cast<const u32x4*>(a.k + off);
-    vx = *reinterpret_cast<const u32x4*>(a.v + off);
-  }
-  if (qr < R) qs[qr][qd] = qv * a.scale_log2;  // rows >= `rows` hold zeros
-  __syncthreads();
-
-  // Scores in the exp2 domain: 8-wide partial dots, summed over the 8 lanes
-  // of a key with DPP (xor 1, xor 2, then the 4-lane halves of the row).
-  {
-    const f16x8 kh = __builtin_bit_cast(f16x8, kx);
-    float kf[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) kf[j] = static_cast<float>(kh[j]);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const f32x4 q0 = *reinterpret_cast<const f32x4*>(&qs[r][pt * 8]);
-      const f32x4 q1 = *reinterpret_cast<const f32x4*>(&qs[r][pt * 8 + 4]);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s = __builtin_fmaf(q0[j], kf[j], s);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s = __builtin_fmaf(q1[j], kf[4 + j], s);
-      s = oct_sum(s);
-      if (pt == 0) ps[r][kl] = valid ? s : -INFINITY;
-    }
-    *reinterpret_cast<u32x4*>(&vs[kl][pt * 8]) = vx;
-  }
-  __syncthreads();
-
-  // Chunk softmax statistics: one wave per row.
-  const int wave = tid >> 6, lane = tid & 63;
-  if (wave < R) {
-    const int r = wave;
-    float x[kKpl], mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kKpl; ++i) {
-      x[i] = ps[r][lane + 64 * i];
-      mx = fmaxf(mx, x[i]);
-    }
-    mx = wave_max(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kKpl; ++i) {
-      const float p = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[i] - mx);
-      ps[r][lane + 64 * i] = p;
-      sum += p;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      mrow[r] = mx;
-      lrow[r] = sum;
-    }
-  }
-  __syncthreads();
-
-  // P V over the chunk: thread (key group kg, d) sums 8 keys for every row.
-  {
-    const int d = tid & 63, kg = tid >> 6;
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-#pragma unroll
-    for (int i = 0; i < kChunk / kKeyGroups; ++i) {
-      const int kk = kg * (kChunk / kKeyGroups) + i;
-      const float vv = static_cast<float>(vs[kk][d]);
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = __builtin_fmaf(ps[r][kk], vv, acc[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) red[kg][r][d] = acc[r];
-  }
-  __syncthreads();
-
-  // Thread (row qr, d qd) of the first rows*64 threads owns one output
-  // element: its sum over the key groups.
   const bool own = qr < rows;
-  float pv = 0.f;
+  float pv = 0.f, M = -INFINITY, Lsum = 0.f;
   if (own) {
 #pragma unroll
-    for (int kg = 0; kg < kKeyGroups; ++kg) pv += red[kg][qr][qd];
+    for (int w = 0; w < kMWaves; ++w) M = fmaxf(M, wm[w][qr]);
+    // Waves without a visible key hold m = -inf, l = 0 and zero partials.
+#pragma unroll
+    for (int w = 0; w < kMWaves; ++w) {
+      const float mw = wm[w][qr];
+      const float al = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+      Lsum = __builtin_fmaf(wl[w][qr], al, Lsum);
+      pv = __builtin_fmaf(red[w][qr][qd] + red[w][qr + 8][qd], al, pv);
+    }
   }
   if (a.n_splits == 1) {
-    // The whole row in one workgroup: normalize and store directly.
-    if (own) {
-      const float l = lrow[qr];
-      a.o[static_cast<int64_t>(g * rows + qr) * a.o_rs + h * 64 + qd] = l > 0.f ? pv * (1.f / l) : 0.f;
-    }
+    if (own)
+      a.o[static_cast<int64_t>(g * rows + qr) * a.o_rs + h * 64 + qd] = Lsum > 0.f ? pv * (1.f / Lsum) : 0.f;
     return;
   }
 
   const int gh = g * a.n_heads + h;
   float* mine = a.part + (static_cast<int64_t>(gh) * a.n_splits + split) * rows * kPart;
   if (own) st_agent(mine + qr * kPart + 4 + qd, pv);
-  if (tid < rows) {
-    st_agent(mine + tid * kPart, mrow[tid]);
-    st_agent(mine + tid * kPart + 1, lrow[tid]);
+  if (own && qd == 0) {
+    st_agent(mine + qr * kPart, M);
+    st_agent(mine + qr * kPart + 1, Lsum);
   }
   // Every wave waits until its agent-scope stores are performed, so the
   // counter increment below is ordered after all of this workgroup's partials.
@@ -332,7 +363,7 @@ size_t decode_counter_words(int n_groups, int n_heads) {
 
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s) {
   if (a.n_groups <= 0 || a.n_splits <= 0) return hipSuccess;
-  const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(kWgThreads);
+  const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(64 * kMWaves);
   switch (a.rows_per_group) {
     case 1: hipLaunchKernelGGL(decode_f16<1>, grid, block, 0, s, a); break;
     case 2: hipLaunchKernelGGL(decode_f16<2>, grid, block, 0, s, a); break;
