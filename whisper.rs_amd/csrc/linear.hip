@@ -430,6 +430,169 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
   }
 }
 
+// K7m (gemv_f16w_mfma): the same product for 3..8 x rows on the matrix pipe.
+//   W is read in tiles of T <= 16 features: lane (c, g) of a wave loads 16
+//   bytes of feature c (columns 32 s + 8 g ..) per 32-column k-step s, which is
+//   the A operand of a 16x16x32 f16 MFMA as loaded; lanes c >= T repeat the
+//   tile's first feature (no extra traffic) and feed zeros. T = ceil(n_out /
+//   n_CU) up to 16, so that a d x d matrix still spreads over every CU. The 8
+//   waves of a workgroup split the k-steps of a tile; each wave keeps 5
+//   k-steps (one register batch) of W in flight ahead of the MFMAs, the next
+//   tile's first batch included.
+//   x is staged once per workgroup into LDS as f16: row b (f32) is scaled by
+//   2^sh_b (its max into [2^14, 2^15)) and split into a high part (B column
+//   b) and a low part (B column 8 + b), so the products carry ~2^-22 relative
+//   error; f16 x is exact in the high half alone. Rows are padded by 16 bytes,
+//   which puts the 16 rows a ds_read_b128 phase touches on distinct banks.
+//   The waves' 16x16 partial tiles meet in LDS (double-buffered, one barrier
+//   per tile); thread (feature, b) adds the 8 waves' high and low columns,
+//   scales by 2^-sh_b, adds the bias and stores.
+constexpr int kGmWaves = 8;
+constexpr int kGmKB = 5;          // 32-column k-steps per wave per register batch
+constexpr int kGmRedPitch = 20;   // LDS pitch (floats) of one wave's 16x16 partial tile
+constexpr int kGmRedFloats = 16 * kGmRedPitch;
+constexpr size_t kGmStaticLds = sizeof(float) * (2 * kGmWaves * kGmRedFloats + 8);
+constexpr size_t kGmMaxDynLds = 160 * 1024 - kGmStaticLds;
+
+__device__ inline float gm_pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
+__device__ inline int gm_clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
+
+__device__ inline float wave_max64(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+
+template <typename XT, typename OutT>
+__global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int T) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 gxs[];  // [parts * nt][n_in + 8]
+  __shared__ __attribute__((aligned(16))) float red[2][kGmWaves][kGmRedFloats];
+  __shared__ float dn[8];
+
+  constexpr bool kSplit = sizeof(XT) == 4;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int grp = blockIdx.y;
+  const int nt = a.n_tokens, n_in = a.n_in, n_out = a.n_out;
+  const int pitch = n_in + 8;
+  const _Float16* w = a.w[grp];
+  const int ks_total = n_in >> 5;
+  const int s_per = (ks_total + kGmWaves - 1) / kGmWaves;
+  const int ks0 = min(wave * s_per, ks_total), ks1 = min(ks0 + s_per, ks_total);
+  const int n_batches = (s_per + kGmKB - 1) / kGmKB;
+  const int n_tiles = (n_out + T - 1) / T;
+  const bool arow = col < T;
+  const u32x4 zero4 = {0, 0, 0, 0};
+
+  // One batch of W loads; k-steps past the wave's range re-read its last
+  // k-step (in bounds) and are not multiplied.
+  auto load_batch = [&](int tile, int bj, u32x4 (&wv)[kGmKB]) {
+    const int r = min(tile * T + (arow ? col : 0), n_out - 1);
+    const _Float16* wr = w + static_cast<int64_t>(r) * n_in + 8 * kg;
+#pragma unroll
+    for (int u = 0; u < kGmKB; ++u) {
+      const int ks = min(ks0 + bj * kGmKB + u, ks_total - 1);
+      wv[u] = *reinterpret_cast<const u32x4*>(wr + 32 * ks);
+    }
+  };
+
+  int tile = blockIdx.x;
+  u32x4 wv[kGmKB];
+  load_batch(tile, 0, wv);  // in flight while x is staged
+
+  if (wave < nt) {
+    const XT* xr = static_cast<const XT*>(a.x) + static_cast<int64_t>(wave) * a.x_rs;
+    int sh = 0;
+    if constexpr (kSplit) {
+      float amax = 0.f;
+      for (int k = 8 * lane; k < n_in; k += 512) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(xr + k);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(xr + k + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(lo[j]), fabsf(hi[j])));
+      }
+      amax = wave_max64(amax);
+      const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+      sh = e_max == 0 ? 0 : gm_clamp_exp(141 - e_max);
+    }
+    const float up = gm_pow2(sh);
+    for (int k = 8 * lane; k < n_in; k += 512) {
+      f16x8 hv, lv;
+      if constexpr (kSplit) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(xr + k);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = (j < 4 ? x0[j] : x1[j - 4]) * up;
+          const _Float16 h = static_cast<_Float16>(v);
+          hv[j] = h;
+          lv[j] = static_cast<_Float16>(v - static_cast<float>(h));
+        }
+        *reinterpret_cast<f16x8*>(&gxs[(nt + wave) * pitch + k]) = lv;
+      } else {
+        hv = *reinterpret_cast<const f16x8*>(xr + k);
+      }
+      *reinterpret_cast<f16x8*>(&gxs[wave * pitch + k]) = hv;
+    }
+    if (lane == 0) dn[wave] = gm_pow2(gm_clamp_exp(-sh));
+  }
+  __syncthreads();
+
+  // B column c < 8: high part of x row c; c >= 8: low part of row c - 8;
+  // absent rows (and the low half for f16 x) are zero.
+  const int beam = col & 7;
+  const bool bvalid = beam < nt && (kSplit || col < 8);
+  const _Float16* xb = gxs + (bvalid ? (col < 8 ? beam : nt + beam) * pitch : 0) + 8 * kg;
+  const f16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  OutT* out = reinterpret_cast<OutT*>(a.out[grp]);
+  const float* bias = a.bias[grp];
+  int par = 0;
+  for (; tile < n_tiles; tile += gridDim.x) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int bj = 0; bj < n_batches; ++bj) {
+      u32x4 cur[kGmKB];
+#pragma unroll
+      for (int u = 0; u < kGmKB; ++u) cur[u] = arow ? wv[u] : zero4;
+      if (bj + 1 < n_batches)
+        load_batch(tile, bj + 1, wv);
+      else if (tile + static_cast<int>(gridDim.x) < n_tiles)
+        load_batch(tile + gridDim.x, 0, wv);
+#pragma unroll
+      for (int u = 0; u < kGmKB; ++u) {
+        const int ks = ks0 + bj * kGmKB + u;
+        if (ks < ks1) {  // wave-uniform
+          const f16x8 bx = bvalid ? *reinterpret_cast<const f16x8*>(xb + 32 * ks) : zero8;
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[u]), bx, acc,
+                                                       0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[par][wave][(4 * kg + i) * kGmRedPitch + col] = acc[i];
+    __syncthreads();
+    if (tid < 128) {
+      const int r = tid >> 3, b = tid & 7;
+      const int row = tile * T + r;
+      if (r < T && b < nt && row < n_out) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int w8 = 0; w8 < kGmWaves; ++w8)
+          sacc += red[par][w8][r * kGmRedPitch + b] + red[par][w8][r * kGmRedPitch + b + 8];
+        float v = sacc * dn[b];
+        if (bias) v += bias[row];
+        out[static_cast<int64_t>(b) * a.out_rs + static_cast<int64_t>(row >> 6) * a.out_hs +
+            (row & 63)] = static_cast<OutT>(v);
+      }
+    }
+    par ^= 1;
+  }
+}
+
 // f32 rows -> [hi | mid | lo] f16 rows of 3 n_in, plus each row's 2^-shift.
 // One wave per row.
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
@@ -478,6 +641,42 @@ hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStre
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  // Three or more x rows: the matrix-pipe kernel (one or two rows read the
+  // staged x cheaply enough that the FMA kernel's wider spread wins).
+  const size_t gm_lds = static_cast<size_t>(x_dt == kF32 ? 2 : 1) * a.n_tokens * (a.n_in + 8) * 2;
+  if (a.n_tokens >= 3 && (a.n_in & 31) == 0 && gm_lds <= kGmMaxDynLds &&
+      (x_dt == kF32 || x_dt == kF16)) {
+    const int T = std::max(1, std::min(16, (a.n_out + n_cu - 1) / n_cu));
+    const int n_tiles = (a.n_out + T - 1) / T;
+    const size_t total = gm_lds + kGmStaticLds;
+    const int per_cu = std::max(1, std::min(2, static_cast<int>((160 * 1024) / total)));
+    const dim3 ggrid(std::min(n_tiles, n_cu * per_cu), a.n_groups), gblock(64 * kGmWaves);
+#define WRS_GM(XT, OT)                                                                        \
+  {                                                                                           \
+    static const hipError_t attr = hipFuncSetAttribute(                                       \
+        reinterpret_cast<const void*>(&gemv_f16w_mfma<XT, OT>),                               \
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGmMaxDynLds));          \
+    if (attr != hipSuccess) return attr;                                                      \
+    hipLaunchKernelGGL((gemv_f16w_mfma<XT, OT>), ggrid, gblock, gm_lds, s, a, T);             \
+  }
+    if (x_dt == kF32) {
+      switch (out_dt) {
+        case kF32: WRS_GM(float, float); break;
+        case kF16: WRS_GM(float, _Float16); break;
+        case kBF16: WRS_GM(float, __bf16); break;
+        default: return hipErrorInvalidValue;
+      }
+    } else {
+      switch (out_dt) {
+        case kF32: WRS_GM(_Float16, float); break;
+        case kF16: WRS_GM(_Float16, _Float16); break;
+        case kBF16: WRS_GM(_Float16, __bf16); break;
+        default: return hipErrorInvalidValue;
+      }
+    }
+#undef WRS_GM
+    return hipGetLastError();
+  }
   // Up to kGemvSmallOut features: one feature per wave, so that the matrix
   // spreads over ~n_out / 8 CUs; beyond it 4 features per wave share each
   // staged x read.
