@@ -213,6 +213,19 @@ int wrs_linear(wrs_attn_ctx *ctx, int x_dtype, const void *x, size_t x_len,
                size_t n_in, size_t n_out, int out_dtype, void *out, size_t out_len,
                int64_t out_row_stride, int64_t out_head_stride);
 
+/* Several projections of one input in one launch (replaces the consecutive
+ * LinearWeight::linear calls on one normalized input at
+ * crates/whisper/src/decoder.rs:597-611: self-attention q, k and v). Group g
+ * computes out[g](t, r) = w[g][r] . x[t] + bias[g][r] exactly as wrs_linear
+ * does; all groups share x, n_out and the output layout. bias may be NULL, or
+ * hold NULL entries; out_len[g] is out[g]'s length in elements.
+ * n_groups <= 64. */
+int wrs_linear_group(wrs_attn_ctx *ctx, int x_dtype, const void *x, size_t x_len,
+                     int64_t x_row_stride, size_t n_groups, const void *const *w,
+                     const float *const *bias, size_t n_tokens, size_t n_in, size_t n_out,
+                     int out_dtype, void *const *out, const size_t *out_len,
+                     int64_t out_row_stride, int64_t out_head_stride);
+
 /* pub fn layer_norm(input, gamma, beta, eps, num_tokens, d_model, output)
  * -- crates/tensor/src/ops/norm.rs:116-143 (asserts :124-127), device f32 rows;
  * the output may be rounded to f16 / bf16 for a following projection.

@@ -261,3 +261,34 @@ def test_cross_projection_into_arena(wrs, orc, ctx):
                         n_audio, H, dm)
     assert np.abs(host(out) - ref).max() <= TOL16
     arena.close()
+
+
+@pytest.mark.parametrize("n_tokens,x_dt", [(5, "f32"), (1, "f16"), (8, "f32"), (200, "f32"),
+                                            (70, "f16")])
+def test_linear_group_equals_separate_calls(wrs, ctx, n_tokens, x_dt):
+    """The q, k, v projections of one input in one launch (decoder.rs:597-611)
+    give bit-for-bit the outputs of three wrs_linear calls; the k projection
+    has no bias, as in the reference."""
+    note(f"linear group T={n_tokens} x={x_dt}")
+    n_in, n_out = 384, 384
+    rng = np.random.default_rng(n_tokens + 3)
+    x = rng.standard_normal((n_tokens, n_in)).astype(np.float32)
+    xd = dev(x) if x_dt == "f32" else torch.from_numpy(x).half().cuda()
+    ws = [torch.from_numpy(_weights(n_out, n_in, 40 + i)).cuda() for i in range(3)]
+    bs = [dev(rng.standard_normal(n_out).astype(np.float32)), None,
+          dev(rng.standard_normal(n_out).astype(np.float32))]
+    outs = [torch.full((n_tokens, n_out), float("nan"), device="cuda") for _ in range(3)]
+    wrs.linear_group(xd, ws, bs, outs, ctx=ctx)
+    for w, b, o in zip(ws, bs, outs):
+        ref = torch.full((n_tokens, n_out), float("nan"), device="cuda")
+        wrs.linear(xd, w, b, ref, ctx=ctx)
+        assert torch.equal(o.cpu(), ref.cpu())
+
+
+def test_linear_group_rejects_bad_arguments(wrs, ctx):
+    note("linear group errors")
+    x = torch.zeros((2, 64), device="cuda")
+    w = torch.zeros((64, 64), dtype=torch.float16, device="cuda")
+    short = torch.zeros((2, 32), device="cuda")
+    with pytest.raises(AssertionError, match="shorter"):  # the reference asserts lengths
+        wrs.linear_group(x, [w, w], None, [torch.zeros((2, 64), device="cuda"), short], ctx=ctx)

@@ -35,7 +35,7 @@ __all__ = [
     "Context", "KvArena", "ExtensionMissing", "Layout", "flash_attention_2",
     "multi_head_attention", "single_token_mha_d64", "mha_with_cache", "prefill",
     "token_major", "default_context", "header_symbols", "Q_TILE", "KV_TILE", "linear",
-    "layer_norm", "gelu_inplace",
+    "linear_group", "layer_norm", "gelu_inplace",
 ]
 
 
@@ -204,6 +204,37 @@ def linear(x, w, bias, out, *, out_row_stride=None, out_head_stride=64, ctx=None
                                   None if bias is None else bias.data_ptr(), n_tokens, n_in,
                                   n_out, _dtype_code(out), out.data_ptr(), _span(out), rs,
                                   out_head_stride), "linear")
+
+
+def linear_group(x, ws, biases, outs, *, out_row_stride=None, out_head_stride=64, ctx=None):
+    """Several LinearWeight::linear projections of one input in one launch
+    (the self-attention q, k, v of crates/whisper/src/decoder.rs:597-611):
+    ``outs[g]`` = ``x`` W_g^T + ``biases[g]``, each exactly as :func:`linear`.
+    ``ws`` are float16 [n_out][n_in] CUDA tensors of one shape; ``biases`` is
+    None or a list with float32 tensors or None entries; ``outs`` share dtype
+    and shape."""
+    ctx = ctx or default_context()
+    n = len(ws)
+    assert n == len(outs) and n > 0
+    n_tokens, n_in = x.shape[0], x.shape[-1]
+    n_out = ws[0].shape[0]
+    for w in ws:
+        assert tuple(w.shape) == (n_out, n_in) and str(w.dtype) == "torch.float16"
+    biases = list(biases) if biases is not None else [None] * n
+    for b in biases:
+        assert b is None or (b.numel() == n_out and str(b.dtype) == "torch.float32")
+    for o in outs:
+        assert o.dtype == outs[0].dtype
+    rs = n_out if out_row_stride is None else out_row_stride
+    vp = ctypes.c_void_p
+    w_arr = (vp * n)(*[w.data_ptr() for w in ws])
+    b_arr = (vp * n)(*[None if b is None else b.data_ptr() for b in biases])
+    o_arr = (vp * n)(*[o.data_ptr() for o in outs])
+    len_arr = (ctypes.c_size_t * n)(*[_span(o) for o in outs])
+    ctx.check(_L.lib().wrs_linear_group(ctx.handle, _dtype_code(x), x.data_ptr(), _span(x),
+                                        x.stride(0) if x.dim() > 1 else n_in, n, w_arr, b_arr,
+                                        n_tokens, n_in, n_out, _dtype_code(outs[0]), o_arr,
+                                        len_arr, rs, out_head_stride), "linear_group")
 
 
 def layer_norm(x, gamma, beta, eps, out, ctx=None):

@@ -930,18 +930,17 @@ bool aligned_out(const void* p, int dt, int64_t rs, int64_t hs) {
   return (reinterpret_cast<uintptr_t>(p) % need) == 0 && rs % 4 == 0 && hs % 4 == 0;
 }
 
-}  // namespace
-
-extern "C" {
-
-int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_t x_row_stride,
-               const void* w, const float* bias, size_t n_tokens, size_t n_in, size_t n_out,
-               int out_dtype, void* out, size_t out_len, int64_t out_row_stride,
-               int64_t out_head_stride) {
-  if (!c) return WRS_EINVAL;
-  std::lock_guard<std::mutex> lk(c->mu);
+// W_g x + bias_g for g < n_groups weight matrices of one shape against one
+// input, in one launch (the caller holds c->mu). bias may be NULL, or hold
+// NULL entries.
+int linear_impl(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_t x_row_stride,
+                int n_groups, const void* const* w, const float* const* bias, size_t n_tokens,
+                size_t n_in, size_t n_out, int out_dtype, void* const* out,
+                const size_t* out_len, int64_t out_row_stride, int64_t out_head_stride) {
   if (n_tokens == 0 || n_out == 0) return WRS_OK;  // quant.rs:430-432
-  if (!x || !w || !out) return fail(c, WRS_EINVAL, "null argument");
+  if (!x) return fail(c, WRS_EINVAL, "null argument");
+  for (int gi = 0; gi < n_groups; ++gi)
+    if (!w[gi] || !out[gi]) return fail(c, WRS_EINVAL, "null argument");
   // quant.rs:424-425: x holds num_tokens rows of cols, output num_tokens * rows
   if (x_row_stride < 0 || out_row_stride < 0 || out_head_stride < 0)
     return fail(c, WRS_EINVAL, "negative stride");
@@ -952,10 +951,13 @@ int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_
       (n_tokens - 1) * static_cast<size_t>(out_row_stride) +
       std::max(last_g * static_cast<size_t>(out_head_stride) + (n_out - 1) % 64,
                last_g ? (last_g - 1) * static_cast<size_t>(out_head_stride) + 63 : 0);
-  if (out_len <= max_off) return fail(c, WRS_EINVAL, "out shorter than the written range");
+  for (int gi = 0; gi < n_groups; ++gi)
+    if (out_len[gi] <= max_off) return fail(c, WRS_EINVAL, "out shorter than the written range");
   if (out_dtype != WRS_F32 && out_dtype != WRS_F16 && out_dtype != WRS_BF16)
     return fail(c, WRS_EINVAL, "unknown output dtype");
-  if (reinterpret_cast<uintptr_t>(w) & 15) return fail(c, WRS_EUNSUPPORTED, "w needs 16-byte alignment");
+  for (int gi = 0; gi < n_groups; ++gi)
+    if (reinterpret_cast<uintptr_t>(w[gi]) & 15)
+      return fail(c, WRS_EUNSUPPORTED, "w needs 16-byte alignment");
   DeviceGuard g(c->device);
   if (n_tokens <= static_cast<size_t>(wrs::kGemvMaxRows) &&
       n_tokens * n_in <= static_cast<size_t>(wrs::kGemvXFloats)) {
@@ -976,30 +978,66 @@ int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_
     gv.n_tokens = static_cast<int>(n_tokens);
     gv.n_in = static_cast<int>(n_in);
     gv.n_out = static_cast<int>(n_out);
-    gv.n_groups = 1;
+    gv.n_groups = n_groups;
     gv.out_rs = out_row_stride;
     gv.out_hs = out_head_stride;
-    gv.w[0] = static_cast<const _Float16*>(w);
-    gv.bias[0] = bias;
-    gv.out[0] = out;
+    for (int gi = 0; gi < n_groups; ++gi) {
+      gv.w[gi] = static_cast<const _Float16*>(w[gi]);
+      gv.bias[gi] = bias ? bias[gi] : nullptr;
+      gv.out[gi] = out[gi];
+    }
     WRS_HIP(c, wrs::launch_gemv_f16w(gv, static_cast<wrs::DType>(x_dtype),
                                      static_cast<wrs::DType>(out_dtype), c->stream));
     return WRS_OK;
   }
-  if (!aligned_out(out, out_dtype, out_row_stride, out_head_stride) ||
-      (bias && (reinterpret_cast<uintptr_t>(bias) & 15)))
-    return fail(c, WRS_EUNSUPPORTED, "bias needs 16-byte, out 4-element alignment");
+  for (int gi = 0; gi < n_groups; ++gi)
+    if (!aligned_out(out[gi], out_dtype, out_row_stride, out_head_stride) ||
+        (bias && bias[gi] && (reinterpret_cast<uintptr_t>(bias[gi]) & 15)))
+      return fail(c, WRS_EUNSUPPORTED, "bias needs 16-byte, out 4-element alignment");
   wrs::LinearArgs a{};
   int rc = linear_prepare(c, x_dtype, x, x_row_stride, n_tokens, n_in, n_out, a);
   if (rc) return rc;
-  a.n_groups = 1;
+  a.n_groups = n_groups;
   a.out_rs = out_row_stride;
   a.out_hs = out_head_stride;
-  a.w[0] = static_cast<const _Float16*>(w);
-  a.bias[0] = bias;
-  a.out[0] = out;
+  for (int gi = 0; gi < n_groups; ++gi) {
+    a.w[gi] = static_cast<const _Float16*>(w[gi]);
+    a.bias[gi] = bias ? bias[gi] : nullptr;
+    a.out[gi] = out[gi];
+  }
   WRS_HIP(c, wrs::launch_linear_f16w(a, static_cast<wrs::DType>(out_dtype), c->stream));
   return WRS_OK;
+}
+
+
+}  // namespace
+
+extern "C" {
+
+int wrs_linear(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_t x_row_stride,
+               const void* w, const float* bias, size_t n_tokens, size_t n_in, size_t n_out,
+               int out_dtype, void* out, size_t out_len, int64_t out_row_stride,
+               int64_t out_head_stride) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  return linear_impl(c, x_dtype, x, x_len, x_row_stride, 1, &w, &bias, n_tokens, n_in, n_out,
+                     out_dtype, &out, &out_len, out_row_stride, out_head_stride);
+}
+
+int wrs_linear_group(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len,
+                     int64_t x_row_stride, size_t n_groups, const void* const* w,
+                     const float* const* bias, size_t n_tokens, size_t n_in, size_t n_out,
+                     int out_dtype, void* const* out, const size_t* out_len,
+                     int64_t out_row_stride, int64_t out_head_stride) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (n_groups == 0 || n_tokens == 0 || n_out == 0) return WRS_OK;
+  if (!w || !out || !out_len) return fail(c, WRS_EINVAL, "null argument");
+  if (n_groups > static_cast<size_t>(wrs::kMaxLinearGroups))
+    return fail(c, WRS_EINVAL, "more weight matrices than one launch takes");
+  return linear_impl(c, x_dtype, x, x_len, x_row_stride, static_cast<int>(n_groups), w, bias,
+                     n_tokens, n_in, n_out, out_dtype, out, out_len, out_row_stride,
+                     out_head_stride);
 }
 
 int wrs_layer_norm(wrs_attn_ctx* c, const float* x, size_t x_len, const float* gamma,

@@ -235,6 +235,11 @@ class DecoderWeightStream:
     def weight_bytes(self) -> int:
         return sum(r * c * 2 for r, c in self.matrices())
 
+    def launches(self) -> int:
+        """q, k and v share one grouped launch per layer; every other projection
+        is a launch of its own."""
+        return (len(self.matrices()) - 1) - 2 * self.n_layers + 1
+
 
 LARGE_DECODE_WEIGHTS = DecoderWeightStream(
     "whisper-large-v3 decoder step projections, beam 5 (32 layers + vocabulary)", 5, 1280, 32,
