@@ -412,11 +412,13 @@ def measure_traffic(only: str, kernel_tag: str, extra: list[str]):
                 log(f"traffic: {counter} pass failed (rc={r.returncode})")
                 return None
             db = sqlite3.connect(str(dbs[0]))
-            rows = db.execute("select kernel_name, avg(value) from counters_collection "
+            rows = db.execute("select kernel_name, avg(value), max(value) from counters_collection "
                               "where counter_name = ? group by kernel_name", (counter,)).fetchall()
             db.close()
-            kern = [v for n, v in rows if kernel_tag in n]
-            copy = [v for n, v in rows if "copy" in n.lower() or "elementwise" in n.lower()]
+            kern = [v for n, v, _ in rows if kernel_tag in n]
+            # the calibration copy is the largest dispatch of its kernel: other,
+            # smaller copies (input set-up) can share the kernel's name
+            copy = [vmax for n, _, vmax in rows if "copy" in n.lower() or "elementwise" in n.lower()]
             if not kern or not copy or max(copy) <= 0:
                 log(f"traffic: {counter}: kernels not found in the profile")
                 return None
