@@ -272,6 +272,71 @@ def bench_weight_stream(wrs, W, ctx, reps):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / reps
+    # The same step with its LayerNorms (decoder.rs:586-594, :660-668, :737-745, the
+    # final one before the vocabulary) and the MLP GELU (:753): as separate launches,
+    # then fused into the projections (wrs_linear_fused).
+    d = cfg.d_model
+    lng = torch.randn(d, generator=gen, device="cuda") * 0.1 + 1.0
+    lnb = torch.randn(d, generator=gen, device="cuda") * 0.1
+    normed = torch.empty((cfg.beams, d), device="cuda")
+    xres = xs[d]
+    hid = outs[4 * d]
+    wl = [seq[i][1] for i in range(len(seq))]
+
+    def layer_weights(layer):
+        first = layer * per_layer
+        return wl[first:first + per_layer]
+
+    def step_unfused():
+        for layer in range(cfg.n_layers):
+            q, k, v, o, cq, co, m0, m2 = layer_weights(layer)
+            wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
+            wrs.linear_group(normed, [q, k, v], None, qkv_outs, ctx=ctx)
+            wrs.linear(xres, o, None, outs[d], ctx=ctx)
+            wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
+            wrs.linear(normed, cq, None, outs[d], ctx=ctx)
+            wrs.linear(xres, co, None, outs[d], ctx=ctx)
+            wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
+            wrs.linear(normed, m0, None, hid, ctx=ctx)
+            wrs.gelu_inplace(hid, ctx=ctx)
+            wrs.linear(hid, m2, None, outs[d], ctx=ctx)
+        wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
+        wrs.linear(normed, wl[-1], None, outs[cfg.n_vocab], ctx=ctx)
+
+    def step_fused():
+        ln = (lng, lnb, 1e-5)
+        for layer in range(cfg.n_layers):
+            q, k, v, o, cq, co, m0, m2 = layer_weights(layer)
+            wrs.linear_fused(xres, [q, k, v], None, qkv_outs, ln=ln, ctx=ctx)
+            wrs.linear(xres, o, None, outs[d], ctx=ctx)
+            wrs.linear_fused(xres, [cq], None, [outs[d]], ln=ln, ctx=ctx)
+            wrs.linear(xres, co, None, outs[d], ctx=ctx)
+            wrs.linear_fused(xres, [m0], None, [hid], ln=ln, act="gelu", ctx=ctx)
+            wrs.linear(hid, m2, None, outs[d], ctx=ctx)
+        wrs.linear_fused(xres, [wl[-1]], None, [outs[cfg.n_vocab]], ln=ln, ctx=ctx)
+
+    norms = {}
+    for name, fn, launches in (("unfused", step_unfused, cfg.launches() + 4 * cfg.n_layers + 1),
+                               ("fused", step_fused, cfg.launches())):
+        fn()
+        torch.cuda.synchronize()
+        gn = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gn):
+            ctx.use_torch_stream()
+            fn()
+        ctx.use_torch_stream()
+        for _ in range(3):
+            gn.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            gn.replay()
+        end.record()
+        torch.cuda.synchronize()
+        norms[name] = {"ms_per_step": round(start.elapsed_time(end) / reps, 4),
+                       "launches_per_step": launches}
+        log(f"weight stream with norms, {name}: {norms[name]['ms_per_step']} ms, "
+            f"{launches} launches")
     # the vocabulary projection alone (the largest single stream)
     xv, wv, ov = seq[-1]
     for _ in range(10):
@@ -285,7 +350,7 @@ def bench_weight_stream(wrs, W, ctx, reps):
     ms_vocab = start.elapsed_time(end) / reps
     vocab_bytes = cfg.n_vocab * cfg.d_model * 2
     return cfg, ms, cfg.weight_bytes() / (ms * 1e-3) / 1e9, ms_vocab, \
-        vocab_bytes / (ms_vocab * 1e-3) / 1e9
+        vocab_bytes / (ms_vocab * 1e-3) / 1e9, norms
 
 
 def bench_rows(wrs, ctx, reps):
@@ -570,7 +635,7 @@ def main():
         calibration_copy()
         return
     if args.only == "stream":
-        _, sms, sgbs, vms, vgbs = bench_weight_stream(wrs, W, ctx, args.stream_reps)
+        _, sms, sgbs, vms, vgbs, snorms = bench_weight_stream(wrs, W, ctx, args.stream_reps)
         calibration_copy()
         log(f"stream only: step {sms:.3f} ms, {sgbs:.1f} GB/s; vocabulary {vms * 1e3:.1f} us, "
             f"{vgbs:.1f} GB/s")
@@ -586,7 +651,7 @@ def main():
     lcfg = W.LARGE_QKV_F16
     lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
     lms32, ltf32 = bench_linear(wrs, W.LARGE_QKV_F32, ctx, args.linear_reps)
-    scfg, sms, sgbs, vms, vgbs = bench_weight_stream(wrs, W, ctx, args.stream_reps)
+    scfg, sms, sgbs, vms, vgbs, snorms = bench_weight_stream(wrs, W, ctx, args.stream_reps)
     rows = bench_rows(wrs, ctx, args.rows_reps)
     log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
     host_slice = bench_host_slice(wrs, W, ctx)
@@ -672,6 +737,7 @@ def main():
                          "unit": "GB/s", "frac": round(sgbs / PEAK_HBM_GBS, 4), "traffic": None},
             "vocabulary_projection": {"us": round(vms * 1e3, 2), "GBps": round(vgbs, 1),
                                       "frac_hbm": round(vgbs / PEAK_HBM_GBS, 4)},
+            "with_layer_norms_and_gelu": snorms,
         },
         "row_kernels": rows,
         "host_slice": host_slice,

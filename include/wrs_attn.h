@@ -226,6 +226,28 @@ int wrs_linear_group(wrs_attn_ctx *ctx, int x_dtype, const void *x, size_t x_len
                      int out_dtype, void *const *out, const size_t *out_len,
                      int64_t out_row_stride, int64_t out_head_stride);
 
+/* Activations for wrs_linear_fused. */
+#define WRS_ACT_NONE 0
+#define WRS_ACT_GELU 1 /* crates/tensor/src/ops/gelu.rs:11-23, applied in f32 */
+
+/* layer_norm -> linear (one or more weight groups) -> optional GELU, as one
+ * launch for decode-sized batches (replaces, at crates/whisper/src/decoder.rs,
+ * the layer_norm of :586-594 with the q/k/v linears of :597-611, that of
+ * :660-668 with the cross-attention q linear, and that of :737-745 with mlp0
+ * and the gelu_inplace of :753). The values equal wrs_layer_norm (f32 out) on
+ * x, then wrs_linear_group on the normalized rows, then wrs_gelu_inplace on
+ * each output (before rounding when out_dtype is f16/bf16). x is f32;
+ * ln_gamma and ln_beta (16-byte aligned, n_in values) are both NULL to skip
+ * the norm; activation is WRS_ACT_NONE or WRS_ACT_GELU. Batches above 8 rows
+ * (or x beyond the weight-stream kernel's LDS) run the norm as its own
+ * launch. */
+int wrs_linear_fused(wrs_attn_ctx *ctx, const float *x, size_t x_len, int64_t x_row_stride,
+                     const float *ln_gamma, const float *ln_beta, float ln_eps,
+                     size_t n_groups, const void *const *w, const float *const *bias,
+                     size_t n_tokens, size_t n_in, size_t n_out, int activation,
+                     int out_dtype, void *const *out, const size_t *out_len,
+                     int64_t out_row_stride, int64_t out_head_stride);
+
 /* pub fn layer_norm(input, gamma, beta, eps, num_tokens, d_model, output)
  * -- crates/tensor/src/ops/norm.rs:116-143 (asserts :124-127), device f32 rows;
  * the output may be rounded to f16 / bf16 for a following projection.

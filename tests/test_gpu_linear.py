@@ -292,3 +292,49 @@ def test_linear_group_rejects_bad_arguments(wrs, ctx):
     short = torch.zeros((2, 32), device="cuda")
     with pytest.raises(AssertionError, match="shorter"):  # the reference asserts lengths
         wrs.linear_group(x, [w, w], None, [torch.zeros((2, 64), device="cuda"), short], ctx=ctx)
+
+
+@pytest.mark.parametrize("n_tokens,n_groups,act,out_dt", [
+    (5, 3, None, torch.float32), (1, 1, None, torch.float32), (2, 1, "gelu", torch.float32),
+    (5, 1, "gelu", torch.float32), (8, 2, "gelu", torch.float16), (3, 1, None, torch.bfloat16),
+    (40, 3, None, torch.float32), (40, 1, "gelu", torch.float32)])
+def test_linear_fused_equals_unfused_calls(wrs, ctx, n_tokens, n_groups, act, out_dt):
+    """layer_norm -> linear group -> gelu in one launch (decoder.rs:586-611,
+    :737-753) gives bit for bit what wrs_layer_norm, wrs_linear_group and
+    wrs_gelu_inplace give one after another (GELU in f32, then the output
+    rounding); 40 rows take the batched path with the norm as its own launch."""
+    note(f"linear fused T={n_tokens} groups={n_groups} act={act} out={out_dt}")
+    n_in, n_out = 1280, 384
+    rng = np.random.default_rng(n_tokens * 13 + n_groups)
+    x = (2.0 * rng.standard_normal((n_tokens, n_in)) + 0.5).astype(np.float32)
+    gamma = dev((1.0 + 0.1 * rng.standard_normal(n_in)).astype(np.float32))
+    beta = dev((0.1 * rng.standard_normal(n_in)).astype(np.float32))
+    ws = [torch.from_numpy(_weights(n_out, n_in, 70 + i)).cuda() for i in range(n_groups)]
+    bs = [dev(rng.standard_normal(n_out).astype(np.float32)) if i % 2 == 0 else None
+          for i in range(n_groups)]
+    outs = [torch.full((n_tokens, n_out), float("nan"), dtype=out_dt, device="cuda")
+            for _ in range(n_groups)]
+    xd = dev(x)
+    wrs.linear_fused(xd, ws, bs, outs, ln=(gamma, beta, 1e-5), act=act, ctx=ctx)
+    normed = torch.empty((n_tokens, n_in), device="cuda")
+    wrs.layer_norm(xd, gamma, beta, 1e-5, normed, ctx=ctx)
+    for w, b, o in zip(ws, bs, outs):
+        ref = torch.empty((n_tokens, n_out), device="cuda")
+        wrs.linear(normed, w, b, ref, ctx=ctx)
+        if act == "gelu":
+            wrs.gelu_inplace(ref, ctx=ctx)
+        assert torch.equal(o.cpu(), ref.to(out_dt).cpu())
+
+
+def test_linear_fused_rejects_half_norm(wrs, ctx):
+    note("linear fused errors")
+    x = torch.zeros((2, 64), device="cuda")
+    w = torch.zeros((64, 64), dtype=torch.float16, device="cuda")
+    g = torch.ones(64, device="cuda")
+    with pytest.raises(AssertionError, match="gamma and beta"):
+        wrs._L.lib()  # the library loads
+        ctx.check(wrs._L.lib().wrs_linear_fused(
+            ctx.handle, x.data_ptr(), x.numel(), 64, g.data_ptr(), None, 1e-5, 1,
+            (wrs.ctypes.c_void_p * 1)(w.data_ptr()), None, 2, 64, 64, 0, 0,
+            (wrs.ctypes.c_void_p * 1)(torch.zeros((2, 64), device="cuda").data_ptr()),
+            (wrs.ctypes.c_size_t * 1)(128), 64, 64), "linear_fused")

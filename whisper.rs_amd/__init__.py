@@ -35,7 +35,7 @@ __all__ = [
     "Context", "KvArena", "ExtensionMissing", "Layout", "flash_attention_2",
     "multi_head_attention", "single_token_mha_d64", "mha_with_cache", "prefill",
     "token_major", "default_context", "header_symbols", "Q_TILE", "KV_TILE", "linear",
-    "linear_group", "layer_norm", "gelu_inplace",
+    "linear_group", "linear_fused", "layer_norm", "gelu_inplace",
 ]
 
 
@@ -235,6 +235,48 @@ def linear_group(x, ws, biases, outs, *, out_row_stride=None, out_head_stride=64
                                         x.stride(0) if x.dim() > 1 else n_in, n, w_arr, b_arr,
                                         n_tokens, n_in, n_out, _dtype_code(outs[0]), o_arr,
                                         len_arr, rs, out_head_stride), "linear_group")
+
+
+def linear_fused(x, ws, biases, outs, *, ln=None, act=None, out_row_stride=None,
+                 out_head_stride=64, ctx=None):
+    """layer_norm -> linear (one or more weight groups) -> GELU in one launch for
+    decode-sized batches (decoder.rs:586-611, :660-668, :737-753).
+
+    ``x`` float32 [n_tokens][n_in]; ``ln`` None or (gamma, beta, eps) with float32
+    CUDA tensors of n_in values; ``act`` None or "gelu". The values equal
+    :func:`layer_norm` (float32 out), then :func:`linear_group`, then
+    :func:`gelu_inplace` on each output, the GELU taken in float32 before any
+    rounding to ``outs``' dtype."""
+    ctx = ctx or default_context()
+    assert str(x.dtype) == "torch.float32"
+    n = len(ws)
+    assert n == len(outs) and n > 0
+    n_tokens, n_in = x.shape[0], x.shape[-1]
+    n_out = ws[0].shape[0]
+    for w in ws:
+        assert tuple(w.shape) == (n_out, n_in) and str(w.dtype) == "torch.float16"
+    biases = list(biases) if biases is not None else [None] * n
+    for b in biases:
+        assert b is None or (b.numel() == n_out and str(b.dtype) == "torch.float32")
+    for o in outs:
+        assert o.dtype == outs[0].dtype
+    if ln is not None:
+        gamma, beta, eps = ln
+        assert gamma.numel() == n_in and beta.numel() == n_in  # norm.rs:123-124
+    else:
+        gamma, beta, eps = None, None, 0.0
+    codes = {None: 0, "gelu": 1}
+    rs = n_out if out_row_stride is None else out_row_stride
+    vp = ctypes.c_void_p
+    w_arr = (vp * n)(*[w.data_ptr() for w in ws])
+    b_arr = (vp * n)(*[None if b is None else b.data_ptr() for b in biases])
+    o_arr = (vp * n)(*[o.data_ptr() for o in outs])
+    len_arr = (ctypes.c_size_t * n)(*[_span(o) for o in outs])
+    ctx.check(_L.lib().wrs_linear_fused(
+        ctx.handle, x.data_ptr(), _span(x), x.stride(0) if x.dim() > 1 else n_in,
+        None if gamma is None else gamma.data_ptr(), None if beta is None else beta.data_ptr(),
+        float(eps), n, w_arr, b_arr, n_tokens, n_in, n_out, codes[act], _dtype_code(outs[0]),
+        o_arr, len_arr, rs, out_head_stride), "linear_fused")
 
 
 def layer_norm(x, gamma, beta, eps, out, ctx=None):

@@ -81,6 +81,9 @@ _SIGNATURES = {
     "wrs_linear_group": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _sz, ctypes.POINTER(_vp),
                                 ctypes.POINTER(_vp), _sz, _sz, _sz, _int, ctypes.POINTER(_vp),
                                 _szp, ctypes.c_int64, ctypes.c_int64]),
+    "wrs_linear_fused": (_int, [_vp, _vp, _sz, ctypes.c_int64, _vp, _vp, ctypes.c_float, _sz,
+                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), _sz, _sz, _sz, _int, _int,
+                                ctypes.POINTER(_vp), _szp, ctypes.c_int64, ctypes.c_int64]),
     "wrs_layer_norm": (_int, [_vp, _vp, _sz, _vp, _vp, ctypes.c_float, _sz, _sz, _int, _vp, _sz]),
     "wrs_gelu_inplace": (_int, [_vp, _vp, _sz]),
     "wrs_kv_set_cross_proj": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _sz,

@@ -126,23 +126,16 @@ __global__ __launch_bounds__(64 * kLnWaves) void layer_norm_rows(const float* x,
   }
 }
 
-__device__ inline float gelu1(float x) {
-#pragma clang fp contract(off)
-  const float kA = 0.044715f, kS = 0.7978846f;  // gelu.rs:3-4
-  const float inner = kS * x * (1.0f + kA * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
-}
-
 __global__ __launch_bounds__(256) void gelu_f32(float* data, int64_t n) {
   const int64_t n4 = n / 4;
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += gridDim.x * 256ll) {
     f32x4 v = reinterpret_cast<f32x4*>(data)[i];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = gelu1(v[j]);
+    for (int j = 0; j < 4; ++j) v[j] = gelu_tanh(v[j]);
     reinterpret_cast<f32x4*>(data)[i] = v;
   }
   for (int64_t i = 4 * n4 + blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll)
-    data[i] = gelu1(data[i]);
+    data[i] = gelu_tanh(data[i]);
 }
 
 }  // namespace

@@ -37,6 +37,7 @@ namespace wrs {
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -262,6 +263,10 @@ __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
                    acc[i][j][4 * g + 3]};
         v *= rs;
         if (bias) v += *reinterpret_cast<const f32x4*>(bias + r);
+        if (a.act == kActGelu) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+        }
         store4<OutT>(orow_p + static_cast<int64_t>(r >> 6) * a.out_hs + (r & 63), v);
       }
   }
@@ -301,6 +306,82 @@ __device__ inline float wave_sum64(float v) {
   return v + __shfl_xor(v, 32);
 }
 
+// LayerNorm of one f32 row by one wave, in the arithmetic of layer_norm_rows
+// (elementwise.hip, norm.rs:116-143): lane partials over k = 4 lane + 256 i,
+// mean, then the variance around it, each reduced with wave_sum64; so the
+// normalized values equal that kernel's output bit for bit.
+__device__ inline void ln_row_stats(const float* xr, int d, float eps, float& mean,
+                                    float& inv_std) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.0f;
+  for (int k = 4 * lane; k < d; k += 256) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(xr + k);
+    s += (v[0] + v[1]) + (v[2] + v[3]);
+  }
+  mean = wave_sum64(s) / static_cast<float>(d);
+  float q = 0.0f;
+  for (int k = 4 * lane; k < d; k += 256) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(xr + k);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q = fmaf(v[j] - mean, v[j] - mean, q);
+  }
+  const float var = wave_sum64(q) / static_cast<float>(d);
+  inv_std = 1.0f / sqrtf(var + eps);
+}
+__device__ inline f32x4 ln_apply(const float* xr, const float* g, const float* b, int k,
+                                 float mean, float inv_std) {
+  const f32x4 v = *reinterpret_cast<const f32x4*>(xr + k);
+  const f32x4 gg = *reinterpret_cast<const f32x4*>(g + k);
+  const f32x4 bb = *reinterpret_cast<const f32x4*>(b + k);
+  f32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = fmaf((v[j] - mean) * inv_std, gg[j], bb[j]);
+  return o;
+}
+
+// Rows of up to 256 * kLnCache values live in registers: lane l holds
+// columns 4 l + 256 i in v[i] (zeros past d). The loads are issued first
+// (ln_row_load), the arithmetic follows (ln_row_norm), with the arithmetic
+// of ln_row_stats / ln_apply exactly.
+constexpr int kLnCache = 8;
+__device__ inline void ln_row_load(const float* xr, const float* g, const float* b, int d,
+                                   f32x4 (&v)[kLnCache], f32x4 (&gg)[kLnCache],
+                                   f32x4 (&bb)[kLnCache]) {
+  const int lane = threadIdx.x & 63;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kLnCache; ++i) {
+    const int k = 4 * lane + 256 * i;
+    const bool in = k < d;
+    v[i] = in ? *reinterpret_cast<const f32x4*>(xr + k) : z;
+    if (g) {
+      gg[i] = in ? *reinterpret_cast<const f32x4*>(g + k) : z;
+      bb[i] = in ? *reinterpret_cast<const f32x4*>(b + k) : z;
+    }
+  }
+}
+__device__ inline void ln_row_norm(int d, float eps, f32x4 (&v)[kLnCache],
+                                   const f32x4 (&gg)[kLnCache], const f32x4 (&bb)[kLnCache]) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kLnCache; ++i) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+  const float mean = wave_sum64(s) / static_cast<float>(d);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kLnCache; ++i) {
+    if (4 * lane + 256 * i >= d) break;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q = fmaf(v[i][j] - mean, v[i][j] - mean, q);
+  }
+  const float var = wave_sum64(q) / static_cast<float>(d);
+  const float inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < kLnCache; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i][j] = fmaf((v[i][j] - mean) * inv_std, gg[i][j], bb[i][j]);
+}
+
 template <int NT, int kGemvRowsPerWave, typename XT, typename OutT>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[kGemvXFloats];
@@ -332,8 +413,32 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
   if (g4 < n_groups4) load_w(g4, 0, wv);  // in flight while x is staged
 
   // Stage x: row b at xs[b * n_in ..], 8 columns per thread and step, the
-  // 16-byte loads of 4 steps in flight before their stores.
-  {
+  // 16-byte loads of 4 steps in flight before their stores. With a fused
+  // LayerNorm, wave b normalizes row b instead.
+  if constexpr (sizeof(XT) == 4) {
+    if (a.ln_g) {
+      if (wave < NT) {
+        const float* xr = static_cast<const float*>(a.x) + static_cast<int64_t>(wave) * a.x_rs;
+        if (n_in <= 256 * kLnCache) {
+          f32x4 y[kLnCache], gg[kLnCache], bb[kLnCache];
+          ln_row_load(xr, a.ln_g, a.ln_b, n_in, y, gg, bb);
+          ln_row_norm(n_in, a.ln_eps, y, gg, bb);
+#pragma unroll
+          for (int i = 0; i < kLnCache; ++i) {
+            const int k = 4 * lane + 256 * i;
+            if (k < n_in) *reinterpret_cast<f32x4*>(&xs[wave * n_in + k]) = y[i];
+          }
+        } else {
+          float mean, inv_std;
+          ln_row_stats(xr, n_in, a.ln_eps, mean, inv_std);
+          for (int k = 4 * lane; k < n_in; k += 256)
+            *reinterpret_cast<f32x4*>(&xs[wave * n_in + k]) =
+                ln_apply(xr, a.ln_g, a.ln_b, k, mean, inv_std);
+        }
+      }
+    }
+  }
+  if (!a.ln_g) {
     const int n8 = NT * n_in / 8;
     for (int e0 = tid; e0 < n8; e0 += 4 * 64 * kGemvWaves) {
       float v[4][8];
@@ -423,6 +528,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
         for (int b = 0; b < NT; ++b)
           if (b == lane) v = acc[i][b];
         if (bias) v += bias[r];
+        if (a.act == kActGelu) v = gelu_tanh(v);
         out[static_cast<int64_t>(lane) * a.out_rs + static_cast<int64_t>(r >> 6) * a.out_hs +
             (r & 63)] = static_cast<OutT>(v);
       }
@@ -466,7 +572,7 @@ __device__ inline float wave_max64(float v) {
   return fmaxf(v, __shfl_xor(v, 32));
 }
 
-template <typename XT, typename OutT>
+template <typename XT, typename OutT, bool kLn>
 __global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int T) {
   extern __shared__ __attribute__((aligned(16))) _Float16 gxs[];  // [parts * nt][n_in + 8]
   __shared__ __attribute__((aligned(16))) float red[2][kGmWaves][kGmRedFloats];
@@ -500,11 +606,84 @@ __global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int 
     }
   };
 
+  // f32 rows of up to 256 * kLnCache values are loaded into registers before
+  // the first weight batch is issued, so that their wait does not include it
+  // (loads complete in order); the arithmetic depends on a value defined after
+  // both.
   int tile = blockIdx.x;
   u32x4 wv[kGmKB];
+  const bool reg_row = kSplit && n_in <= 256 * kLnCache;
+  f32x4 xv[kLnCache], gg[kLnCache], bb[kLnCache];
+  const float* xr32 = static_cast<const float*>(a.x) + static_cast<int64_t>(wave) * a.x_rs;
+  if (reg_row && wave < nt)
+    ln_row_load(xr32, kLn ? a.ln_g : nullptr, a.ln_b, n_in, xv, gg, bb);
   load_batch(tile, 0, wv);  // in flight while x is staged
+  float one;
+  __asm__ volatile("v_mov_b32 %0, 1.0" : "=v"(one) : : "memory");
 
-  if (wave < nt) {
+  if (reg_row && wave < nt) {
+#pragma unroll
+    for (int i = 0; i < kLnCache; ++i) xv[i] *= one;
+    if constexpr (kLn) ln_row_norm(n_in, a.ln_eps, xv, gg, bb);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < kLnCache; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(xv[i][j]));  // zeros past n_in
+    amax = wave_max64(amax);
+    const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+    const int sh = e_max == 0 ? 0 : gm_clamp_exp(141 - e_max);
+    const float up = gm_pow2(sh);
+#pragma unroll
+    for (int i = 0; i < kLnCache; ++i) {
+      const int k = 4 * lane + 256 * i;
+      if (k >= n_in) break;
+      f16x4v hv, lv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v = xv[i][j] * up;
+        const _Float16 h = static_cast<_Float16>(v);
+        hv[j] = h;
+        lv[j] = static_cast<_Float16>(v - static_cast<float>(h));
+      }
+      *reinterpret_cast<f16x4v*>(&gxs[wave * pitch + k]) = hv;
+      *reinterpret_cast<f16x4v*>(&gxs[(nt + wave) * pitch + k]) = lv;
+    }
+    if (lane == 0) dn[wave] = gm_pow2(gm_clamp_exp(-sh));
+  }
+  if constexpr (kSplit) {
+    if (kLn && !reg_row && wave < nt) {
+      // Longer rows with a fused LayerNorm: statistics, then two passes.
+      const float* xr = xr32;
+      float mean, inv_std;
+      ln_row_stats(xr, n_in, a.ln_eps, mean, inv_std);
+      float amax = 0.f;
+      for (int k = 4 * lane; k < n_in; k += 256) {
+        const f32x4 y = ln_apply(xr, a.ln_g, a.ln_b, k, mean, inv_std);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(y[j]));
+      }
+      amax = wave_max64(amax);
+      const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+      const int sh = e_max == 0 ? 0 : gm_clamp_exp(141 - e_max);
+      const float up = gm_pow2(sh);
+      for (int k = 4 * lane; k < n_in; k += 256) {
+        const f32x4 y = ln_apply(xr, a.ln_g, a.ln_b, k, mean, inv_std);
+        f16x4v hv, lv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = y[j] * up;
+          const _Float16 h = static_cast<_Float16>(v);
+          hv[j] = h;
+          lv[j] = static_cast<_Float16>(v - static_cast<float>(h));
+        }
+        *reinterpret_cast<f16x4v*>(&gxs[wave * pitch + k]) = hv;
+        *reinterpret_cast<f16x4v*>(&gxs[(nt + wave) * pitch + k]) = lv;
+      }
+      if (lane == 0) dn[wave] = gm_pow2(gm_clamp_exp(-sh));
+    }
+  }
+  if (wave < nt && !reg_row && !kLn) {
     const XT* xr = static_cast<const XT*>(a.x) + static_cast<int64_t>(wave) * a.x_rs;
     int sh = 0;
     if constexpr (kSplit) {
@@ -585,6 +764,7 @@ __global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int 
           sacc += red[par][w8][r * kGmRedPitch + b] + red[par][w8][r * kGmRedPitch + b + 8];
         float v = sacc * dn[b];
         if (bias) v += bias[row];
+        if (a.act == kActGelu) v = gelu_tanh(v);
         out[static_cast<int64_t>(b) * a.out_rs + static_cast<int64_t>(row >> 6) * a.out_hs +
             (row & 63)] = static_cast<OutT>(v);
       }
@@ -646,19 +826,36 @@ hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStre
   const size_t gm_lds = static_cast<size_t>(x_dt == kF32 ? 2 : 1) * a.n_tokens * (a.n_in + 8) * 2;
   if (a.n_tokens >= 3 && (a.n_in & 31) == 0 && gm_lds <= kGmMaxDynLds &&
       (x_dt == kF32 || x_dt == kF16)) {
-    const int T = std::max(1, std::min(16, (a.n_out + n_cu - 1) / n_cu));
-    const int n_tiles = (a.n_out + T - 1) / T;
-    const size_t total = gm_lds + kGmStaticLds;
-    const int per_cu = std::max(1, std::min(2, static_cast<int>((160 * 1024) / total)));
-    const dim3 ggrid(std::min(n_tiles, n_cu * per_cu), a.n_groups), gblock(64 * kGmWaves);
-#define WRS_GM(XT, OT)                                                                        \
+    // Tiles of T features, T chosen so that the tiles of all groups just
+    // cover one workgroup per CU (a d x d matrix measured fastest that way:
+    // two smaller tiles per CU stage x twice); up to as many workgroups as fit
+    // at once (LDS and registers decide) share larger matrices, looping over
+    // tiles.
+    const dim3 gblock(64 * kGmWaves);
+#define WRS_GM_L(XT, OT, LN)                                                                  \
   {                                                                                           \
+    const void* fn = reinterpret_cast<const void*>(&gemv_f16w_mfma<XT, OT, LN>);              \
     static const hipError_t attr = hipFuncSetAttribute(                                       \
-        reinterpret_cast<const void*>(&gemv_f16w_mfma<XT, OT>),                               \
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGmMaxDynLds));          \
+        fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGmMaxDynLds));      \
     if (attr != hipSuccess) return attr;                                                      \
-    hipLaunchKernelGGL((gemv_f16w_mfma<XT, OT>), ggrid, gblock, gm_lds, s, a, T);             \
+    int per_cu = 1;                                                                           \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, gblock.x, gm_lds) !=         \
+            hipSuccess ||                                                                     \
+        per_cu < 1)                                                                           \
+      per_cu = 1;                                                                             \
+    const int64_t rows = static_cast<int64_t>(a.n_out) * a.n_groups;                         \
+    const int T = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(16, (rows + n_cu - 1) / n_cu))); \
+    const int n_tiles = (a.n_out + T - 1) / T;                                                \
+    const dim3 ggrid(std::min(n_tiles, n_cu * std::min(per_cu, 2)), a.n_groups);              \
+    hipLaunchKernelGGL((gemv_f16w_mfma<XT, OT, LN>), ggrid, gblock, gm_lds, s, a, T);         \
   }
+#define WRS_GM(XT, OT)                 \
+  if (a.ln_g) {                        \
+    WRS_GM_L(XT, OT, true)             \
+  } else {                             \
+    WRS_GM_L(XT, OT, false)            \
+  }
+#define WRS_GM16(XT, OT) WRS_GM_L(XT, OT, false)
     if (x_dt == kF32) {
       switch (out_dt) {
         case kF32: WRS_GM(float, float); break;
@@ -667,14 +864,17 @@ hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStre
         default: return hipErrorInvalidValue;
       }
     } else {
+      if (a.ln_g) return hipErrorInvalidValue;  // the fused LayerNorm takes f32 rows
       switch (out_dt) {
-        case kF32: WRS_GM(_Float16, float); break;
-        case kF16: WRS_GM(_Float16, _Float16); break;
-        case kBF16: WRS_GM(_Float16, __bf16); break;
+        case kF32: WRS_GM16(_Float16, float); break;
+        case kF16: WRS_GM16(_Float16, _Float16); break;
+        case kBF16: WRS_GM16(_Float16, __bf16); break;
         default: return hipErrorInvalidValue;
       }
     }
+#undef WRS_GM16
 #undef WRS_GM
+#undef WRS_GM_L
     return hipGetLastError();
   }
   // Up to kGemvSmallOut features: one feature per wave, so that the matrix

@@ -34,6 +34,8 @@ struct wrs_attn_ctx {
   size_t cap_part_bytes = 0;
   void* lin_x = nullptr;  // projections: split f16 rows of f32 activations + row scales
   size_t lin_x_bytes = 0;
+  float* ln_x = nullptr;  // fused projections above the weight-stream size: normalized rows
+  size_t ln_x_bytes = 0;
 };
 
 struct wrs_kv {
@@ -316,6 +318,7 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
   if (c->counters) (void)hipFree(c->counters);
   if (c->cap_part) (void)hipFree(c->cap_part);
   if (c->lin_x) (void)hipFree(c->lin_x);
+  if (c->ln_x) (void)hipFree(c->ln_x);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -936,7 +939,9 @@ bool aligned_out(const void* p, int dt, int64_t rs, int64_t hs) {
 int linear_impl(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64_t x_row_stride,
                 int n_groups, const void* const* w, const float* const* bias, size_t n_tokens,
                 size_t n_in, size_t n_out, int out_dtype, void* const* out,
-                const size_t* out_len, int64_t out_row_stride, int64_t out_head_stride) {
+                const size_t* out_len, int64_t out_row_stride, int64_t out_head_stride,
+                const float* ln_g = nullptr, const float* ln_b = nullptr, float ln_eps = 0.f,
+                int act = wrs::kActNone) {
   if (n_tokens == 0 || n_out == 0) return WRS_OK;  // quant.rs:430-432
   if (!x) return fail(c, WRS_EINVAL, "null argument");
   for (int gi = 0; gi < n_groups; ++gi)
@@ -981,6 +986,10 @@ int linear_impl(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64
     gv.n_groups = n_groups;
     gv.out_rs = out_row_stride;
     gv.out_hs = out_head_stride;
+    gv.ln_g = ln_g;
+    gv.ln_b = ln_b;
+    gv.ln_eps = ln_eps;
+    gv.act = act;
     for (int gi = 0; gi < n_groups; ++gi) {
       gv.w[gi] = static_cast<const _Float16*>(w[gi]);
       gv.bias[gi] = bias ? bias[gi] : nullptr;
@@ -994,9 +1003,21 @@ int linear_impl(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64
     if (!aligned_out(out[gi], out_dtype, out_row_stride, out_head_stride) ||
         (bias && bias[gi] && (reinterpret_cast<uintptr_t>(bias[gi]) & 15)))
       return fail(c, WRS_EUNSUPPORTED, "bias needs 16-byte, out 4-element alignment");
+  if (ln_g) {
+    // Larger batches: the LayerNorm runs as its own launch into scratch rows.
+    int rc = grow(c, reinterpret_cast<void**>(&c->ln_x), &c->ln_x_bytes,
+                  n_tokens * n_in * sizeof(float), false);
+    if (rc) return rc;
+    WRS_HIP(c, wrs::launch_layer_norm(static_cast<const float*>(x), ln_g, ln_b, ln_eps,
+                                      static_cast<int>(n_tokens), static_cast<int>(n_in),
+                                      wrs::kF32, c->ln_x, c->stream));
+    x = c->ln_x;
+    x_row_stride = static_cast<int64_t>(n_in);
+  }
   wrs::LinearArgs a{};
   int rc = linear_prepare(c, x_dtype, x, x_row_stride, n_tokens, n_in, n_out, a);
   if (rc) return rc;
+  a.act = act;
   a.n_groups = n_groups;
   a.out_rs = out_row_stride;
   a.out_hs = out_head_stride;
@@ -1038,6 +1059,30 @@ int wrs_linear_group(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len,
   return linear_impl(c, x_dtype, x, x_len, x_row_stride, static_cast<int>(n_groups), w, bias,
                      n_tokens, n_in, n_out, out_dtype, out, out_len, out_row_stride,
                      out_head_stride);
+}
+
+int wrs_linear_fused(wrs_attn_ctx* c, const float* x, size_t x_len, int64_t x_row_stride,
+                     const float* ln_gamma, const float* ln_beta, float ln_eps, size_t n_groups,
+                     const void* const* w, const float* const* bias, size_t n_tokens,
+                     size_t n_in, size_t n_out, int activation, int out_dtype, void* const* out,
+                     const size_t* out_len, int64_t out_row_stride, int64_t out_head_stride) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (n_groups == 0 || n_tokens == 0 || n_out == 0) return WRS_OK;
+  if (!w || !out || !out_len) return fail(c, WRS_EINVAL, "null argument");
+  if (n_groups > static_cast<size_t>(wrs::kMaxLinearGroups))
+    return fail(c, WRS_EINVAL, "more weight matrices than one launch takes");
+  if ((ln_gamma == nullptr) != (ln_beta == nullptr))
+    return fail(c, WRS_EINVAL, "layer norm needs both gamma and beta");
+  if (activation != WRS_ACT_NONE && activation != WRS_ACT_GELU)
+    return fail(c, WRS_EINVAL, "unknown activation");
+  if (ln_gamma && ((reinterpret_cast<uintptr_t>(ln_gamma) & 15) ||
+                   (reinterpret_cast<uintptr_t>(ln_beta) & 15)))
+    return fail(c, WRS_EUNSUPPORTED, "gamma and beta need 16-byte alignment");
+  return linear_impl(c, WRS_F32, x, x_len, x_row_stride, static_cast<int>(n_groups), w, bias,
+                     n_tokens, n_in, n_out, out_dtype, out, out_len, out_row_stride,
+                     out_head_stride, ln_gamma, ln_beta, ln_eps,
+                     activation == WRS_ACT_GELU ? wrs::kActGelu : wrs::kActNone);
 }
 
 int wrs_layer_norm(wrs_attn_ctx* c, const float* x, size_t x_len, const float* gamma,

@@ -15,6 +15,19 @@ namespace wrs {
 
 enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
+// Activation applied by a projection's epilogue, in f32 before the output
+// rounding (the reference runs gelu_inplace on the f32 projection output).
+enum Act : int { kActNone = 0, kActGelu = 1 };
+
+// GELU, tanh form, in the reference's order of operations with contraction
+// off (crates/tensor/src/ops/gelu.rs:6-23; constants gelu.rs:3-4).
+__device__ inline float gelu_tanh(float x) {
+#pragma clang fp contract(off)
+  const float kA = 0.044715f, kS = 0.7978846f;
+  const float inner = kS * x * (1.0f + kA * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
 struct Layout {
   int64_t bs;  // batch (window) stride
   int64_t hs;  // head stride
@@ -121,6 +134,7 @@ struct LinearArgs {
   const float* row_scale;  // nullable: 1
   int n_tokens, n_in, n_out, k_total, n_groups;
   int64_t out_rs, out_hs;
+  int act;  // Act, applied after the bias
   const _Float16* w[kMaxLinearGroups];
   const float* bias[kMaxLinearGroups];  // nullable entries
   void* out[kMaxLinearGroups];
@@ -135,6 +149,12 @@ struct GemvArgs {
   int64_t x_rs;
   int n_tokens, n_in, n_out, n_groups;
   int64_t out_rs, out_hs;
+  // Optional LayerNorm of every x row before the product (norm.rs:116-143,
+  // the layer_norm_rows arithmetic exactly; f32 x only): ln_g null = none.
+  const float* ln_g;
+  const float* ln_b;
+  float ln_eps;
+  int act;  // Act, applied after the bias
   const _Float16* w[kMaxLinearGroups];
   const float* bias[kMaxLinearGroups];
   void* out[kMaxLinearGroups];
