@@ -343,7 +343,7 @@ __device__ inline f32x4 ln_apply(const float* xr, const float* g, const float* b
 // columns 4 l + 256 i in v[i] (zeros past d). The loads are issued first
 // (ln_row_load), the arithmetic follows (ln_row_norm), with the arithmetic
 // of ln_row_stats / ln_apply exactly.
-constexpr int kLnCache = 8;
+constexpr int kLnCache = 5;  // 1280 columns: every Whisper d_model
 __device__ inline void ln_row_load(const float* xr, const float* g, const float* b, int d,
                                    f32x4 (&v)[kLnCache], f32x4 (&gg)[kLnCache],
                                    f32x4 (&bb)[kLnCache]) {
