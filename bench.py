@@ -578,6 +578,32 @@ def cpu_baseline_linear(cfg, threads):
                       f"{best * 1e3:.1f} ms"}
 
 
+def cpu_baseline_stream(cfg, threads):
+    """The oracle's f16_linear over one decoder layer's projections for the
+    step's beams (q, k, v, out, cross q, cross out, mlp0, mlp2): f16 weights
+    streamed once per matrix, as f16_gemv_parallel does (quant.rs:392-413)."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    rng = np.random.default_rng(0x5EED)
+    mats = cfg.matrices()[:len(cfg.matrices()[:-1]) // cfg.n_layers]
+    ws = [(rng.standard_normal((r, c)) * c ** -0.5).astype(np.float16) for r, c in mats]
+    xs = {c: np.ascontiguousarray(rng.standard_normal((cfg.beams, c)).astype(np.float32).ravel())
+          for _, c in mats}
+    outs = {r: np.zeros(cfg.beams * r, np.float32) for r, _ in mats}
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for w in ws:
+            r, c = w.shape
+            orc.f16_linear(w, r, c, xs[c], None, cfg.beams, outs[r], n_threads=threads)
+        best = min(best, time.perf_counter() - t0)
+    nbytes = sum(r * c * 2 for r, c in mats)
+    return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"one layer's 8 projections ({nbytes / 1e6:.1f} MB of f16 weights, "
+                      f"{cfg.beams} rows), best of 3, {best * 1e3:.2f} ms"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -671,7 +697,7 @@ def main():
         return None if t is None else round(t["FETCH_SIZE"] + t["WRITE_SIZE"])
 
     threads = min(16, os.cpu_count() or 1)
-    cpu_enc = cpu_dec = cpu_cap = cpu_lin = None
+    cpu_enc = cpu_dec = cpu_cap = cpu_lin = cpu_stream = None
     if not args.no_cpu:
         log(f"cpu baseline: oracle encoder window on {threads} threads")
         cpu_enc = cpu_baseline_encoder(cfg, qkv, threads)
@@ -681,6 +707,8 @@ def main():
         cpu_cap = cpu_baseline_capture(ccfg)
         log(f"cpu baseline: oracle f16_linear, one window, {threads} threads")
         cpu_lin = cpu_baseline_linear(lcfg, threads)
+        log(f"cpu baseline: oracle f16_linear, one decoder layer's projections, {threads} threads")
+        cpu_stream = cpu_baseline_stream(scfg, threads)
 
     line = {
         "metric": METRIC,
@@ -738,6 +766,7 @@ def main():
             "vocabulary_projection": {"us": round(vms * 1e3, 2), "GBps": round(vgbs, 1),
                                       "frac_hbm": round(vgbs / PEAK_HBM_GBS, 4)},
             "with_layer_norms_and_gelu": snorms,
+            "cpu_baseline": cpu_stream,
         },
         "row_kernels": rows,
         "host_slice": host_slice,
