@@ -199,7 +199,7 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, co
  * -> crates/tensor/src/ops/quant.rs:415-473 f16_linear):
  * out(t, r) = W[r] . x[t] + bias[r], W [n_out][n_in] f16 row-major (the ggml
  * halves), bias f32 or NULL, x [n_tokens] rows of n_in (row stride in
- * elements) as f32 (products kept exact) or f16. x_len and out_len are the
+ * elements) as f32 (split into two f16 parts: products to 2^-22) or f16. x_len and out_len are the
  * buffers' lengths in elements, checked like the reference's length asserts
  * (quant.rs:424-425). out(t, r) is written in
  * out_dtype at out + t*out_row_stride + (r/64)*out_head_stride + r%64:

@@ -18,13 +18,14 @@
 //   that each XCD runs a compact block of 4 feature x 8 token tiles at a time.
 //   Measured on the large-v3 fused QKV shape (24000 x 1280 x 3840): this
 //   shape of tile reaches ~85% of the library GEMM on the same box.
-//   f32 activations are made exact on the f16 matrix pipe by a pre-pass
+//   f32 activations go to the f16 matrix pipe through a pre-pass
 //   (linear_split_rows): each row is scaled by a power of two so that its
-//   largest element lies in [2^14, 2^15), then split into three f16 parts
-//   hi + mid + lo that sum to it (parts below 2^-24 of the row maximum are
-//   dropped). The GEMM then runs over k' = 3 n_in with the weight column
-//   k' mod n_in, so every product is exact and only the f32 accumulation
-//   rounds, as in dot_f16_f32 (simd.rs:593-700). The epilogue multiplies by
+//   largest element lies in [2^14, 2^15), then split into two f16 parts
+//   hi + lo that sum to it within 2^-22 relative (2^-25 of the row maximum
+//   where lo is subnormal). The GEMM then runs over k' = 2 n_in with the
+//   weight column k' mod n_in; each product carries at most that 2^-22
+//   relative error, below what one f32 addition of the accumulation
+//   (dot_f16_f32, simd.rs:593-700) already rounds away. The epilogue multiplies by
 //   the row's 2^-shift (exact), adds the f32 bias and stores 4 consecutive
 //   features per lane in the output type, at
 //   out + t * out_rs + (r / 64) * out_hs + r % 64: token-major rows
@@ -773,7 +774,7 @@ __global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int 
   }
 }
 
-// f32 rows -> [hi | mid | lo] f16 rows of 3 n_in, plus each row's 2^-shift.
+// f32 rows -> [hi | lo] f16 rows of 2 n_in, plus each row's 2^-shift.
 // One wave per row.
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
 __device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
@@ -791,15 +792,12 @@ __global__ __launch_bounds__(256) void linear_split_rows(const float* x, int64_t
   const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
   const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
   const float up = pow2(sh);
-  _Float16* dst = xs + static_cast<int64_t>(t) * 3 * n_in;
+  _Float16* dst = xs + static_cast<int64_t>(t) * kSplitParts * n_in;
   for (int k = lane; k < n_in; k += 64) {
     const float v = xr[k] * up;
     const _Float16 h = static_cast<_Float16>(v);
-    const float r1 = v - static_cast<float>(h);
-    const _Float16 m = static_cast<_Float16>(r1);
     dst[k] = h;
-    dst[n_in + k] = m;
-    dst[2 * n_in + k] = static_cast<_Float16>(r1 - static_cast<float>(m));
+    dst[n_in + k] = static_cast<_Float16>(v - static_cast<float>(h));
   }
   if (lane == 0) row_scale[t] = pow2(clamp_exp(-sh));
 }

@@ -897,7 +897,7 @@ int linear_prepare(wrs_attn_ctx* c, int x_dtype, const void* x, int64_t x_rs, si
   if (x_rs < static_cast<int64_t>(n_in)) return fail(c, WRS_EINVAL, "x row stride < n_in");
   // The kernel addresses W and x through buffer resources: 32-bit byte
   // offsets, including the rows past the edge of the last tile.
-  const int64_t xs_rs = x_dtype == WRS_F32 ? 3 * static_cast<int64_t>(n_in) : x_rs;
+  const int64_t xs_rs = x_dtype == WRS_F32 ? wrs::kSplitParts * static_cast<int64_t>(n_in) : x_rs;
   if ((static_cast<int64_t>(n_tokens) + 256) * xs_rs * 2 >= (int64_t{1} << 31) ||
       (static_cast<int64_t>(n_out) + 256) * static_cast<int64_t>(n_in) * 2 >= (int64_t{1} << 31))
     return fail(c, WRS_EUNSUPPORTED, "x or W span beyond the kernel's 2 GiB addressing");
@@ -914,7 +914,7 @@ int linear_prepare(wrs_attn_ctx* c, int x_dtype, const void* x, int64_t x_rs, si
     return WRS_OK;
   }
   if (x_dtype != WRS_F32) return fail(c, WRS_EUNSUPPORTED, "x must be f32 or f16");
-  const size_t split_bytes = align_up(n_tokens * 3 * n_in * 2, 256);
+  const size_t split_bytes = align_up(n_tokens * wrs::kSplitParts * n_in * 2, 256);
   int rc = grow(c, &c->lin_x, &c->lin_x_bytes, split_bytes + n_tokens * 4, false);
   if (rc) return rc;
   auto* xs = static_cast<_Float16*>(c->lin_x);
@@ -922,9 +922,9 @@ int linear_prepare(wrs_attn_ctx* c, int x_dtype, const void* x, int64_t x_rs, si
   WRS_HIP(c, wrs::launch_linear_split(static_cast<const float*>(x), x_rs, a.n_tokens, a.n_in, xs,
                                       scale, c->stream));
   a.x = xs;
-  a.x_rs = 3 * static_cast<int64_t>(n_in);
+  a.x_rs = wrs::kSplitParts * static_cast<int64_t>(n_in);
   a.row_scale = scale;
-  a.k_total = 3 * a.n_in;
+  a.k_total = wrs::kSplitParts * a.n_in;
   return WRS_OK;
 }
 

@@ -122,11 +122,12 @@ hipError_t launch_capture_cross_f16(const CaptureArgs& a, hipStream_t s);
 
 // Projections with f16 weights (quant.rs:415-473 semantics):
 // out(t, r) = row_scale[t] * (W[r] . x'[t]) + bias[r] with W [n_out][n_in] f16
-// and x' [n_tokens][k_total] f16 (k_total = n_in, or 3 n_in for split f32 rows,
-// whose weight column is k' mod n_in). Element (t, r) is stored at
+// and x' [n_tokens][k_total] f16 (k_total = n_in, or kSplitParts n_in for split
+// f32 rows, whose weight column is k' mod n_in). Element (t, r) is stored at
 // out + t*out_rs + (r/64)*out_hs + r%64. Groups share x and differ in W, bias
 // and out (all layers' cross K and V in one launch).
 constexpr int kLinearK = 64;          // n_in must be a multiple of this
+constexpr int kSplitParts = 2;        // f16 parts of a split f32 row: hi, lo
 constexpr int kMaxLinearGroups = 64;
 struct LinearArgs {
   const _Float16* x;
@@ -160,7 +161,7 @@ struct GemvArgs {
   void* out[kMaxLinearGroups];
 };
 hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStream_t s);
-// f32 rows -> [hi | mid | lo] f16 rows (3 n_in each) and per-row 2^-shift.
+// f32 rows -> [hi | lo] f16 rows (kSplitParts n_in each) and per-row 2^-shift.
 hipError_t launch_linear_split(const float* x, int64_t x_rs, int n_tokens, int n_in,
                                _Float16* xs, float* row_scale, hipStream_t s);
 
