@@ -33,6 +33,7 @@
 #include "wrs_internal.hpp"
 
 #include <algorithm>
+#include <atomic>
 
 namespace wrs {
 namespace {
@@ -833,9 +834,13 @@ hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStre
 #define WRS_GM_L(XT, OT, LN)                                                                  \
   {                                                                                           \
     const void* fn = reinterpret_cast<const void*>(&gemv_f16w_mfma<XT, OT, LN>);              \
-    static const hipError_t attr = hipFuncSetAttribute(                                       \
-        fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGmMaxDynLds));      \
-    if (attr != hipSuccess) return attr;                                                      \
+    static std::atomic<uint64_t> attr_set{0};  /* one bit per device */                       \
+    if (dev < 64 && !(attr_set.load(std::memory_order_acquire) & (uint64_t{1} << dev))) {     \
+      const hipError_t e = hipFuncSetAttribute(                                               \
+          fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGmMaxDynLds));    \
+      if (e != hipSuccess) return e;                                                          \
+      attr_set.fetch_or(uint64_t{1} << dev, std::memory_order_acq_rel);                       \
+    }                                                                                         \
     int per_cu = 1;                                                                           \
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, gblock.x, gm_lds) !=         \
             hipSuccess ||                                                                     \
