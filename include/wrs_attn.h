@@ -240,7 +240,7 @@ int wrs_linear_group(wrs_attn_ctx *ctx, int x_dtype, const void *x, size_t x_len
  * ln_gamma and ln_beta (16-byte aligned, n_in values) are both NULL to skip
  * the norm; activation is WRS_ACT_NONE or WRS_ACT_GELU. Batches above 8 rows
  * (or x beyond the weight-stream kernel's LDS) run the norm as its own
- * launch. */
+ * launch and then need packed rows (x_row_stride == n_in). */
 int wrs_linear_fused(wrs_attn_ctx *ctx, const float *x, size_t x_len, int64_t x_row_stride,
                      const float *ln_gamma, const float *ln_beta, float ln_eps,
                      size_t n_groups, const void *const *w, const float *const *bias,

@@ -1005,6 +1005,8 @@ int linear_impl(wrs_attn_ctx* c, int x_dtype, const void* x, size_t x_len, int64
       return fail(c, WRS_EUNSUPPORTED, "bias needs 16-byte, out 4-element alignment");
   if (ln_g) {
     // Larger batches: the LayerNorm runs as its own launch into scratch rows.
+    if (x_row_stride != static_cast<int64_t>(n_in))
+      return fail(c, WRS_EUNSUPPORTED, "a fused layer norm over more than 8 rows needs packed x rows");
     int rc = grow(c, reinterpret_cast<void**>(&c->ln_x), &c->ln_x_bytes,
                   n_tokens * n_in * sizeof(float), false);
     if (rc) return rc;
