@@ -273,9 +273,13 @@ def bench_weight_stream(wrs, W, ctx, reps):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / reps
     # The same step with its LayerNorms (decoder.rs:586-594, :660-668, :737-745, the
-    # final one before the vocabulary) and the MLP GELU (:753): as separate launches,
-    # then fused into the projections (wrs_linear_fused).
+    # final one before the vocabulary), the MLP GELU (:753) and the biases the
+    # reference's projections carry (q, v, out, cross q, cross out, mlp0, mlp2; k and the
+    # vocabulary have none): as separate launches, then fused into the projections
+    # (wrs_linear_fused).
     d = cfg.d_model
+    bd = torch.randn(d, generator=gen, device="cuda") * 0.1
+    b4d = torch.randn(4 * d, generator=gen, device="cuda") * 0.1
     lng = torch.randn(d, generator=gen, device="cuda") * 0.1 + 1.0
     lnb = torch.randn(d, generator=gen, device="cuda") * 0.1
     normed = torch.empty((cfg.beams, d), device="cuda")
@@ -291,15 +295,15 @@ def bench_weight_stream(wrs, W, ctx, reps):
         for layer in range(cfg.n_layers):
             q, k, v, o, cq, co, m0, m2 = layer_weights(layer)
             wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
-            wrs.linear_group(normed, [q, k, v], None, qkv_outs, ctx=ctx)
-            wrs.linear(xres, o, None, outs[d], ctx=ctx)
+            wrs.linear_group(normed, [q, k, v], [bd, None, bd], qkv_outs, ctx=ctx)
+            wrs.linear(xres, o, bd, outs[d], ctx=ctx)
             wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
-            wrs.linear(normed, cq, None, outs[d], ctx=ctx)
-            wrs.linear(xres, co, None, outs[d], ctx=ctx)
+            wrs.linear(normed, cq, bd, outs[d], ctx=ctx)
+            wrs.linear(xres, co, bd, outs[d], ctx=ctx)
             wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
-            wrs.linear(normed, m0, None, hid, ctx=ctx)
+            wrs.linear(normed, m0, b4d, hid, ctx=ctx)
             wrs.gelu_inplace(hid, ctx=ctx)
-            wrs.linear(hid, m2, None, outs[d], ctx=ctx)
+            wrs.linear(hid, m2, bd, outs[d], ctx=ctx)
         wrs.layer_norm(xres, lng, lnb, 1e-5, normed, ctx=ctx)
         wrs.linear(normed, wl[-1], None, outs[cfg.n_vocab], ctx=ctx)
 
@@ -307,12 +311,12 @@ def bench_weight_stream(wrs, W, ctx, reps):
         ln = (lng, lnb, 1e-5)
         for layer in range(cfg.n_layers):
             q, k, v, o, cq, co, m0, m2 = layer_weights(layer)
-            wrs.linear_fused(xres, [q, k, v], None, qkv_outs, ln=ln, ctx=ctx)
-            wrs.linear(xres, o, None, outs[d], ctx=ctx)
-            wrs.linear_fused(xres, [cq], None, [outs[d]], ln=ln, ctx=ctx)
-            wrs.linear(xres, co, None, outs[d], ctx=ctx)
-            wrs.linear_fused(xres, [m0], None, [hid], ln=ln, act="gelu", ctx=ctx)
-            wrs.linear(hid, m2, None, outs[d], ctx=ctx)
+            wrs.linear_fused(xres, [q, k, v], [bd, None, bd], qkv_outs, ln=ln, ctx=ctx)
+            wrs.linear(xres, o, bd, outs[d], ctx=ctx)
+            wrs.linear_fused(xres, [cq], [bd], [outs[d]], ln=ln, ctx=ctx)
+            wrs.linear(xres, co, bd, outs[d], ctx=ctx)
+            wrs.linear_fused(xres, [m0], [b4d], [hid], ln=ln, act="gelu", ctx=ctx)
+            wrs.linear(hid, m2, bd, outs[d], ctx=ctx)
         wrs.linear_fused(xres, [wl[-1]], None, [outs[cfg.n_vocab]], ln=ln, ctx=ctx)
 
     norms = {}

@@ -478,6 +478,14 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
   __syncthreads();
 
   for (; g4 < n_groups4; g4 += stride) {
+    // The group's bias is loaded now, so that its latency hides under the
+    // products instead of following the reduction.
+    float bias_v[kGemvRowsPerWave];
+#pragma unroll
+    for (int i = 0; i < kGemvRowsPerWave; ++i) {
+      const int r = min(g4 * kGemvRowsPerWave + i, a.n_out - 1);
+      bias_v[i] = bias ? bias[r] : 0.0f;
+    }
     float acc[kGemvRowsPerWave][NT];
 #pragma unroll
     for (int i = 0; i < kGemvRowsPerWave; ++i)
@@ -532,7 +540,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_f16w(GemvArgs a) {
 #pragma unroll
         for (int b = 0; b < NT; ++b)
           if (b == lane) v = acc[i][b];
-        if (bias) v += bias[r];
+        if (bias) v += bias_v[i];
         if (a.act == kActGelu) v = gelu_tanh(v);
         out[static_cast<int64_t>(lane) * a.out_rs + static_cast<int64_t>(r >> 6) * a.out_hs +
             (r & 63)] = static_cast<OutT>(v);
@@ -737,6 +745,9 @@ __global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int 
   const float* bias = a.bias[grp];
   int par = 0;
   for (; tile < n_tiles; tile += gridDim.x) {
+    // Bias of the feature this thread stores, loaded under the MFMAs.
+    float bias_v = 0.f;
+    if (bias && tid < 128) bias_v = bias[min(tile * T + min(tid >> 3, T - 1), n_out - 1)];
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int bj = 0; bj < n_batches; ++bj) {
       u32x4 cur[kGmKB];
@@ -768,7 +779,7 @@ __global__ __launch_bounds__(64 * kGmWaves) void gemv_f16w_mfma(GemvArgs a, int 
         for (int w8 = 0; w8 < kGmWaves; ++w8)
           sacc += red[par][w8][r * kGmRedPitch + b] + red[par][w8][r * kGmRedPitch + b + 8];
         float v = sacc * dn[b];
-        if (bias) v += bias[row];
+        if (bias) v += bias_v;
         if (a.act == kActGelu) v = gelu_tanh(v);
         out[static_cast<int64_t>(b) * a.out_rs + static_cast<int64_t>(row >> 6) * a.out_hs +
             (row & 63)] = static_cast<OutT>(v);
