@@ -69,11 +69,15 @@ __global__ __launch_bounds__(64 * kLnWaves) void layer_norm_rows(const float* x,
   const float* xr = x + static_cast<int64_t>(row) * d;
   OutT* orow = out + static_cast<int64_t>(row) * d;
   if constexpr (kCached > 0) {
-    f32x4 v[kCached];
+    // The row, gamma and beta are all requested before the reductions.
+    f32x4 v[kCached], gv[kCached], bv[kCached];
 #pragma unroll
     for (int i = 0; i < kCached; ++i) {
       const int k = 4 * lane + 256 * i;
-      v[i] = k < d ? *reinterpret_cast<const f32x4*>(xr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const bool in = k < d;
+      v[i] = in ? *reinterpret_cast<const f32x4*>(xr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      gv[i] = in ? *reinterpret_cast<const f32x4*>(gamma + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      bv[i] = in ? *reinterpret_cast<const f32x4*>(beta + k) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float s = 0.0f;
 #pragma unroll
@@ -92,11 +96,9 @@ __global__ __launch_bounds__(64 * kLnWaves) void layer_norm_rows(const float* x,
     for (int i = 0; i < kCached; ++i) {
       const int k = 4 * lane + 256 * i;
       if (k >= d) break;
-      const f32x4 g = *reinterpret_cast<const f32x4*>(gamma + k);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(beta + k);
       f32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = fmaf((v[i][j] - mean) * inv_std, g[j], b[j]);
+      for (int j = 0; j < 4; ++j) o[j] = fmaf((v[i][j] - mean) * inv_std, gv[i][j], bv[i][j]);
       store4<OutT>(orow + k, o);
     }
     return;
