@@ -632,7 +632,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the attention path shards across GPUs without exchange; see DESIGN.md)",
+              "(the attention path shards across GPUs by window, utterance or head, "
+              "without exchange)",
               file=sys.stderr)
         sys.exit(2)
 

@@ -5,7 +5,7 @@ The oracle is a C restatement of the reference's CPU attention path
 crates/tensor/src/simd.rs:4-119 and :593-700, crates/tensor/src/ops/quant.rs:343-473,
 crates/whisper/src/decoder.rs:796-892).
 Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
-import this module, and only as the checker or the timed CPU baseline. The
+import this module, and only as the parity reference or the timed CPU baseline. The
 product package (``whisper.rs_amd``) never imports it.
 
 Function names and argument meaning follow the reference; shape violations

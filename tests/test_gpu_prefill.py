@@ -108,7 +108,7 @@ def test_host_slice_edges_and_asserts(wrs, ctx):
         wrs.flash_attention_2(q, q, q, 2, 1, 2, d_model, False, q.copy(), ctx=ctx)
 
 
-# ---- device-resident prefill on the BASELINE-shaped workloads -------------
+# ---- device-resident prefill on the benchmark-shaped workloads ------------
 
 def _encoder_run(wrs, ctx, cfg, q, k, v, dtype, batch=None):
     b = q.shape[0] if batch is None else batch
