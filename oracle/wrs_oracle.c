@@ -3,7 +3,7 @@
  *
  * A C restatement of the reference's CPU algorithm. Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library,
- * and only as the checker / timed baseline. The product library never links
+ * and only as the parity reference / timed baseline. The product library never links
  * or calls it.
  *
  * Reference files restated here (paths relative to the reference root):

@@ -2,7 +2,7 @@
  * CPU oracle for the whisper.rs attention path -- TEST INFRASTRUCTURE ONLY.
  *
  * This is a C restatement of the reference CPU algorithm, used by tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker and
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the parity reference and
  * as the timed CPU baseline. It is never linked into, loaded by or called from
  * the product library (whisper.rs_amd/), which must fail loudly when its HIP
  * build is missing instead of falling back to this code.
