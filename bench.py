@@ -140,6 +140,59 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
     return cfg, us, gbs
 
 
+def bench_decode_self(wrs, W, ctx, reps):
+    """Causal self-attention decode, whisper-small shape (beam 5 slots, 12 heads,
+    valid length 224 of 448): one launch per layer over 12 layers, 8 arenas rotated
+    so that the 330 MB read per round trip is larger than the 256 MB MALL."""
+    import torch
+    cfg = W.SMALL_SELF_DECODE
+    n_layers, U = 12, 8
+    log(f"decode self: building {U} x {n_layers}-layer self caches, length {cfg.ctx}")
+    kvs = [cfg.kv(s) for s in range(cfg.beams)]
+    kd = [(torch.from_numpy(k.astype(np.float32)).cuda(), torch.from_numpy(v.astype(np.float32)).cuda())
+          for k, v in kvs]
+    arenas = []
+    for u in range(U):
+        ar = wrs.KvArena(n_layers, cfg.beams, cfg.n_heads, cfg.max_ctx, 0, ctx=ctx)
+        for s_ in range(cfg.beams):
+            k, v = kd[s_]
+            for layer in range(n_layers):
+                ar.append(layer, s_, k[:cfg.ctx - 1], v[:cfg.ctx - 1])
+            ar.advance(s_, cfg.ctx - 1)
+            for layer in range(n_layers):
+                ar.append(layer, s_, k[cfg.ctx - 1:], v[cfg.ctx - 1:])
+        arenas.append(ar)
+    q = torch.from_numpy(cfg.q()).cuda()
+    outs = torch.zeros((U, n_layers, cfg.beams, cfg.d_model), device="cuda")
+    slots = list(range(cfg.beams))
+
+    def all_layers():
+        for u in range(U):
+            for layer in range(n_layers):
+                arenas[u].decode_self(layer, slots, q, outs[u, layer])
+
+    all_layers()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.use_torch_stream()
+        all_layers()
+    ctx.use_torch_stream()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (reps * U * n_layers)
+    for ar in arenas:
+        ar.close()
+    return cfg, us, cfg.bytes() / (us * 1e-6) / 1e9
+
+
 def bench_capture(wrs, W, ctx, reps, use_graph=True):
     """DTW alignment pass: one capture launch per preset layer, inputs resident."""
     import torch
@@ -653,6 +706,9 @@ def main():
         _, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps, use_graph=not args.eager)
         calibration_copy()
         log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
+        if not args.eager:
+            _, sus, sgbs_ = bench_decode_self(wrs, W, ctx, args.decode_reps)
+            log(f"decode self (whisper-small, length 224): {sus:.3f} us/launch, {sgbs_:.1f} GB/s")
         return
     if args.only == "linear":
         cfgs = (W.LARGE_QKV_F16,) if args.linear_f16_only else (W.LARGE_QKV_F16, W.LARGE_QKV_F32)
@@ -678,6 +734,7 @@ def main():
         return
     cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
+    dscfg, dsus, dsgbs = bench_decode_self(wrs, W, ctx, args.decode_reps)
     ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
     lcfg = W.LARGE_QKV_F16
     lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
@@ -742,6 +799,14 @@ def main():
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic_bytes(dec_traffic)},
             "cpu_baseline": cpu_dec,
+        },
+        "decode_self": {
+            "workload": dscfg.name + f", valid length {dscfg.ctx} of {dscfg.max_ctx}",
+            "value": round(dsgbs, 1), "unit": "GB/s", "us_per_launch": round(dsus, 3),
+            "launches_per_step": 12, "bytes_per_launch": dscfg.bytes(), "dtype": "f16",
+            "roofline": {"bound": "hbm", "achieved": round(dsgbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(dsgbs / PEAK_HBM_GBS, 4),
+                         "traffic": None},
         },
         "capture": {
             "workload": ccfg.name, "value": round(cgbs, 1), "unit": "GB/s",

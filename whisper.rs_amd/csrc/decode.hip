@@ -4,7 +4,9 @@
 //   (replaces crates/tensor/src/ops/attention.rs:246-434 single_token_mha_d64
 //    as called from crates/whisper/src/decoder.rs:636 / :698).
 //   Grid (split, head, group). A workgroup of 8 waves owns kChunk = 128
-//   consecutive keys of one (group, head) plane and ALL query rows of the
+//   consecutive keys (16 waves and 256 keys when that covers the whole
+//   sequence, so that no merge is needed) of one (group, head) plane and ALL
+//   query rows of the
 //   group (the beams of an utterance share the cross-attention plane, so it is
 //   read once per step instead of once per beam). Each wave takes 16 keys,
 //   and every lane issues its q loads and its four 16-byte K/V loads before
@@ -48,8 +50,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;            // exact f32 decode
-constexpr int kChunk = kDecodeChunk;     // keys per workgroup
-constexpr int kMWaves = kChunk / 16;     // one 16-key MFMA tile per wave
 constexpr int kRedPitch = 68;            // LDS pitch (floats) of a wave's 16 output rows
 constexpr int kPart = 68;    // floats per partial row: m, l, 2 pad, acc[64]
 constexpr int kCounterStride = 32;  // 128 bytes between merge counters
@@ -89,10 +89,14 @@ __device__ inline float ld_agent(const float* p) {
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
 __device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
 
-static_assert(kMWaves >= kMaxRowsPerGroup, "one merging wave per query row");
 
-template <int R>
+// kMWaves waves of one 16-key tile each: 8 (128 keys, kDecodeChunk) in
+// general, 16 (kDecodeChunkLong = 256 keys) when that covers the whole
+// sequence, which then needs no split-K merge.
+template <int R, int kMWaves>
 __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
+  static_assert(kMWaves >= kMaxRowsPerGroup, "one merging wave per query row");
+  constexpr int kChunk = 16 * kMWaves;
   __shared__ float red[kMWaves][16][kRedPitch];
   __shared__ float wm[kMWaves][8], wl[kMWaves][8];
   __shared__ int last_flag;
@@ -363,18 +367,26 @@ size_t decode_counter_words(int n_groups, int n_heads) {
 
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s) {
   if (a.n_groups <= 0 || a.n_splits <= 0) return hipSuccess;
-  const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(64 * kMWaves);
+  if (a.chunk != kDecodeChunk && a.chunk != kDecodeChunkLong) return hipErrorInvalidValue;
+  const bool lng = a.chunk == kDecodeChunkLong;
+  const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(lng ? 1024 : 512);
+#define WRS_DEC(R)                                                          \
+  if (lng)                                                                  \
+    hipLaunchKernelGGL((decode_f16<R, 16>), grid, block, 0, s, a);          \
+  else                                                                      \
+    hipLaunchKernelGGL((decode_f16<R, 8>), grid, block, 0, s, a);
   switch (a.rows_per_group) {
-    case 1: hipLaunchKernelGGL(decode_f16<1>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(decode_f16<2>, grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL(decode_f16<3>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(decode_f16<4>, grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL(decode_f16<5>, grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL(decode_f16<6>, grid, block, 0, s, a); break;
-    case 7: hipLaunchKernelGGL(decode_f16<7>, grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL(decode_f16<8>, grid, block, 0, s, a); break;
+    case 1: WRS_DEC(1) break;
+    case 2: WRS_DEC(2) break;
+    case 3: WRS_DEC(3) break;
+    case 4: WRS_DEC(4) break;
+    case 5: WRS_DEC(5) break;
+    case 6: WRS_DEC(6) break;
+    case 7: WRS_DEC(7) break;
+    case 8: WRS_DEC(8) break;
     default: return hipErrorInvalidValue;
   }
+#undef WRS_DEC
   return hipGetLastError();
 }
 

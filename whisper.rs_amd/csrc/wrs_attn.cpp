@@ -246,8 +246,12 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
   a.n_groups = n_groups;
   a.rows_per_group = rows_per_group;
   a.n_heads = n_heads;
-  a.chunk = wrs::kDecodeChunk;
-  a.n_splits = std::max(1, (max_len + wrs::kDecodeChunk - 1) / wrs::kDecodeChunk);
+  // Sequences of 129..256 keys take one 16-wave workgroup per (group, head):
+  // no partials and no merge. Longer ones split into 128-key workgroups.
+  a.chunk = (max_len > wrs::kDecodeChunk && max_len <= wrs::kDecodeChunkLong)
+                ? wrs::kDecodeChunkLong
+                : wrs::kDecodeChunk;
+  a.n_splits = std::max(1, (max_len + a.chunk - 1) / a.chunk);
   a.scale_log2 = 0.125f * 1.4426950408889634f;
   if (a.n_splits > 1) {
     const size_t pb =

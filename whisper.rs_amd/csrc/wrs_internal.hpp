@@ -88,13 +88,14 @@ struct DecodeArgs {
   int64_t goff[kMaxDecodeGroups];  // per-group plane offset (elements)
   int len[kMaxDecodeGroups];       // keys visible to group g
   int n_groups, rows_per_group, n_heads;
-  int chunk;     // keys per workgroup (kDecodeChunk)
+  int chunk;     // keys per workgroup (kDecodeChunk or kDecodeChunkLong)
   int n_splits;  // workgroups per (group, head) = ceil(max len / chunk)
   float scale_log2;  // (1/8) * log2(e)
   float* part;        // scratch: [groups][heads][splits][rows][68]
   unsigned* counters;  // scratch: one per (group, head) every 32 words, zero between launches
 };
 constexpr int kDecodeChunk = 128;
+constexpr int kDecodeChunkLong = 256;  // one workgroup per (group, head) up to this length
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s);
 size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows);
 size_t decode_counter_words(int n_groups, int n_heads);
