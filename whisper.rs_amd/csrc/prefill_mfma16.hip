@@ -37,7 +37,8 @@
 // may lag the true row max; a rescale (move the reference to the row max,
 // scale O and l, form the weights again) happens only when some query's row
 // sum over a step exceeds 2^14, which also bounds every weight inside the f16
-// range. The first step always rescales.
+// range. The first step takes its reference max from its own (masked) scores
+// before forming its weights, so it never forms them twice.
 #include "wrs_internal.hpp"
 
 #include <type_traits>
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   };
   // Lazy rescale (see the file header): after a step's weights are formed,
   // move the reference max when some lane's partial row sum is out of range
-  // (always on the first step), rescale O and l, and form the weights again;
+  // (the first step has already taken its max), rescale O and l, and form the weights again;
   // then fold the step's row sums into l.
   auto settle = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
     bool need = false;
@@ -444,6 +445,18 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       constexpr bool kFull = decltype(full_tag)::value;
       if (kFull || j + 1 < nh) qk(ka, s_out);
       if (!kFull && j >= first_masked) mask_step(j, s_in);
+      if (!kFull && j == 0) {
+        // First step: take the reference max from the (masked) scores now, so
+        // the weights are formed once instead of being redone by the rescale.
+#pragma unroll
+        for (int jb = 0; jb < kQB; ++jb) {
+          float mr = fmaxf(s_in[jb][0], s_in[jb][1]);
+#pragma unroll
+          for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s_in[jb][i]), s_in[jb][i + 1]);
+          const float mx = pair_max(mr) * c;
+          if (mx > m[jb]) m[jb] = mx;
+        }
+      }
       weights(s_in, p_out);
       row_sums(p_out, ls);
       if (kFull || j >= 1) pv(va, p_in);
@@ -549,3 +562,4 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
 }
 
 }  // namespace wrs
+
