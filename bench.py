@@ -13,8 +13,15 @@ layer, 32 layers resident, one launch per layer. Three utterances' caches
 replayed from a HIP graph. Bytes are the unique K/V bytes (read once for all
 beams) plus f32 Q and O.
 
+Timing: each timed encoder leg first runs a time-bounded clock-settle phase
+(SETTLE_SECONDS of the same launch, reported in the line's config), then
+`--warmup` untimed steps, then `--steps` timed steps. Decode legs replay HIP
+graphs of one launch per layer and divide by the launch count.
+
 cpu_baseline: the CPU oracle (a C restatement of the reference path) timed on
-this host on a bounded sample.
+this host on a bounded sample, by the reference's own benchmark method
+(best of 9 after a warm call; encoder legs alternate the tiled kernel with the
+materialized baseline on available_parallelism() threads).
 """
 from __future__ import annotations
 
@@ -52,12 +59,90 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def bench_encoder(wrs, W, ctx, steps, warmup):
+SETTLE_SECONDS = 1.5  # clock-settle phase before the timed encoder steps
+
+
+def settle_clocks(fn, seconds: float = SETTLE_SECONDS) -> int:
+    """Run `fn` (one launch of the timed workload) for `seconds` of wall time.
+
+    MI355X engine clocks settle only after ~300 encoder launches (~75 ms of
+    sustained MFMA load); a fixed launch count warms a short run less than a
+    long one, so the settle phase is bounded by time and reported in the line.
+    """
     import torch
-    cfg = W.LARGE_ENCODER
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    return n
+
+
+def cpu_info() -> dict:
+    """Host CPU model and the thread count the reference would use:
+    std::thread::available_parallelism() is the affinity mask bounded by the
+    cgroup CPU quota (bench_flash_attention_tiled.rs:247-249 uses it)."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    nproc = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, -(-int(q) // int(per)))
+    except (OSError, ValueError):
+        pass
+    threads = min(nproc, quota) if quota else nproc
+    return {"model": model, "nproc": nproc, "cgroup_cpus": quota, "threads": threads}
+
+
+REPS = 9  # bench_flash_attention_tiled.rs:20
+
+
+def time_both(a, b, reps: int = REPS):
+    """bench_flash_attention_tiled.rs:109-134: best of `reps`, the two calls in
+    alternating order so drift and background load bias both equally."""
+    best_a = best_b = float("inf")
+    for rep in range(reps):
+        order = (a, b) if rep % 2 == 0 else (b, a)
+        for f in order:
+            t0 = time.perf_counter()
+            f()
+            dt = time.perf_counter() - t0
+            if f is a:
+                best_a = min(best_a, dt)
+            else:
+                best_b = min(best_b, dt)
+    return best_a, best_b
+
+
+def time_best(a, reps: int = REPS) -> float:
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        a()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True):
+    """One prefill launch over all windows per step, inputs resident in HBM:
+    a time-bounded clock-settle phase, `warmup` untimed steps, then `steps`
+    timed steps between two events on the launch stream."""
+    import torch
+    cfg = cfg or W.LARGE_ENCODER
     log(f"encoder: generating {cfg.name}")
     q, k, v = cfg.inputs()
-    qd, kd, vd = (torch.from_numpy(x).to(torch.bfloat16).cuda() for x in (q, k, v))
+    tdt = torch.bfloat16 if cfg.storage == "bf16" else torch.float16
+    qd, kd, vd = (torch.from_numpy(x).to(tdt).cuda() for x in (q, k, v))
     B, T, dm = cfg.batch, cfg.t, cfg.d_model
     out = torch.empty((B, T, dm), dtype=torch.float32, device="cuda")
     lay = wrs.token_major(T, dm, 64)
@@ -66,6 +151,10 @@ def bench_encoder(wrs, W, ctx, steps, warmup):
         wrs.prefill(qd, kd, vd, out, batch=B, n_heads=cfg.n_heads, t_q=T, t_kv=T, d_head=64,
                     q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
 
+    settled = 0
+    if settle:
+        log(f"encoder: settling clocks for {SETTLE_SECONDS} s")
+        settled = settle_clocks(step)
     log(f"encoder: warmup {warmup}")
     for _ in range(warmup):
         step()
@@ -79,10 +168,31 @@ def bench_encoder(wrs, W, ctx, steps, warmup):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     tflops = cfg.flops() / (ms * 1e-3) / 1e12
-    return cfg, ms, tflops, (q, k, v)
+    log(f"encoder: {cfg.name}: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s "
+        f"({tflops / PEAK_BF16_TFLOPS:.3f} of peak; settle {settled} launches)")
+    return cfg, ms, tflops, (q, k, v), settled
+
+
+def _replay_time_us(g, reps, launches_per_replay):
+    import torch
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (reps * launches_per_replay)
 
 
 def bench_decode(wrs, W, ctx, reps, use_graph=True):
+    """Cross-attention decode, one launch per layer over 32 resident layers,
+    three utterances' caches rotated (737 MB > the 256 MB MALL), replayed
+    from a HIP graph. Beside it, the practical floor of one decode-sized
+    launch: a plain streaming read of the same 7.68 MB per launch
+    (wrs_stream_read), rotated the same way."""
     import torch
     cfg = W.LARGE_CROSS_DECODE
     U = 3  # utterances rotated: 3 x 245.76 MB of cross K/V > 256 MB MALL
@@ -96,13 +206,14 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
         arenas.append(ar)
     qs = torch.from_numpy(np.stack([cfg.q(layer) for layer in range(cfg.n_layers)])).cuda()
     outs = torch.zeros((U, cfg.n_layers, cfg.beams, cfg.d_model), device="cuda")
+    ctx.reserve(n_heads=cfg.n_heads, decode_rows=cfg.beams, decode_keys=cfg.n_audio)
 
     def all_layers():
         for u in range(U):
             for layer in range(cfg.n_layers):
                 arenas[u].decode_cross(layer, qs[layer], outs[u, layer])
 
-    all_layers()  # sizes the scratch outside any capture
+    all_layers()
     torch.cuda.synchronize()
     if not use_graph:  # eager launches (counter passes)
         for _ in range(reps):
@@ -110,7 +221,7 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
         torch.cuda.synchronize()
         for ar in arenas:
             ar.close()
-        return cfg, float("nan"), float("nan")
+        return cfg, float("nan"), float("nan"), None
     eager = outs.clone()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
@@ -122,75 +233,101 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
     torch.cuda.synchronize()
     if not torch.equal(outs, eager):
         raise RuntimeError("graph replay of the decode launches differs from eager")
-    for _ in range(3):
-        g.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     log(f"decode: timing {reps} graph replays of {U * cfg.n_layers} launches")
-    start.record()
-    for _ in range(reps):
-        g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    n_launch = reps * U * cfg.n_layers
-    us = start.elapsed_time(end) * 1e3 / n_launch
+    us = _replay_time_us(g, reps, U * cfg.n_layers)
     gbs = cfg.bytes_per_layer() / (us * 1e-6) / 1e9
+    # the floor: 7.68 MB per launch (two layers' K planes, contiguous)
+    per = 2 * cfg.n_heads * cfg.n_audio * 64 * 2
+    sink = torch.zeros(per // 32768 + 1, device="cuda")
+    bases = [ar.plane_pointers()[2] for ar in arenas]
+
+    def all_reads():
+        for base in bases:
+            for pair in range(cfg.n_layers // 2):
+                ctx.check(ctx._lib.wrs_stream_read(ctx.handle, base + pair * per, per,
+                                                   sink.data_ptr(), sink.numel()),
+                          "wrs_stream_read")
+
+    all_reads()
+    torch.cuda.synchronize()
+    gf = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gf):
+        ctx.use_torch_stream()
+        all_reads()
+    ctx.use_torch_stream()
+    floor_us = _replay_time_us(gf, reps, U * cfg.n_layers // 2)
+    floor = {"bytes_per_launch": per, "us_per_launch": round(floor_us, 3),
+             "GBps": round(per / (floor_us * 1e-6) / 1e9, 1)}
+    log(f"decode: {us:.3f} us/launch ({gbs:.1f} GB/s); single-launch read floor "
+        f"{floor_us:.3f} us ({floor['GBps']} GB/s)")
     for ar in arenas:
         ar.close()
-    return cfg, us, gbs
+    return cfg, us, gbs, floor
 
 
-def bench_decode_self(wrs, W, ctx, reps):
-    """Causal self-attention decode, whisper-small shape (beam 5 slots, 12 heads,
-    valid length 224 of 448): one launch per layer over 12 layers, 8 arenas rotated
-    so that the 330 MB read per round trip is larger than the 256 MB MALL."""
+def bench_decode_self(wrs, W, ctx, reps, lengths=None, eager=False):
+    """Causal self-attention decode, whisper-small shape (beam 5 slots, 12
+    heads, max_ctx 448): one launch per layer over 12 layers, 8 arenas rotated
+    so that the bytes read per round are larger than the 256 MB MALL, at each
+    valid length L (the step's own row included)."""
     import torch
-    cfg = W.SMALL_SELF_DECODE
+    lengths = lengths or W.SELF_DECODE_SWEEP
+    base = W.SMALL_SELF_DECODE
     n_layers, U = 12, 8
-    log(f"decode self: building {U} x {n_layers}-layer self caches, length {cfg.ctx}")
-    kvs = [cfg.kv(s) for s in range(cfg.beams)]
+    maxc = base.max_ctx
+    log(f"decode self: building {U} x {n_layers}-layer self caches of {maxc} rows")
+    full = W.SelfDecode(base.name, base.beams, base.n_heads, maxc)
+    kvs = [full.kv(s) for s in range(base.beams)]
     kd = [(torch.from_numpy(k.astype(np.float32)).cuda(), torch.from_numpy(v.astype(np.float32)).cuda())
           for k, v in kvs]
     arenas = []
     for u in range(U):
-        ar = wrs.KvArena(n_layers, cfg.beams, cfg.n_heads, cfg.max_ctx, 0, ctx=ctx)
-        for s_ in range(cfg.beams):
+        ar = wrs.KvArena(n_layers, base.beams, base.n_heads, maxc, 0, ctx=ctx)
+        for s_ in range(base.beams):
             k, v = kd[s_]
             for layer in range(n_layers):
-                ar.append(layer, s_, k[:cfg.ctx - 1], v[:cfg.ctx - 1])
-            ar.advance(s_, cfg.ctx - 1)
-            for layer in range(n_layers):
-                ar.append(layer, s_, k[cfg.ctx - 1:], v[cfg.ctx - 1:])
+                ar.append(layer, s_, k, v)
+            ar.advance(s_, maxc)
         arenas.append(ar)
-    q = torch.from_numpy(cfg.q()).cuda()
-    outs = torch.zeros((U, n_layers, cfg.beams, cfg.d_model), device="cuda")
-    slots = list(range(cfg.beams))
+    q = torch.from_numpy(base.q()).cuda()
+    outs = torch.zeros((U, n_layers, base.beams, base.d_model), device="cuda")
+    slots = list(range(base.beams))
+    ctx.reserve(n_heads=base.n_heads, decode_rows=base.beams, decode_keys=maxc)
 
     def all_layers():
         for u in range(U):
             for layer in range(n_layers):
                 arenas[u].decode_self(layer, slots, q, outs[u, layer])
 
-    all_layers()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        ctx.use_torch_stream()
+    res = {}
+    for L in lengths:
+        for ar in arenas:
+            for s_ in slots:
+                # the rows stay in the planes: reset the length, then advance
+                # it so that the step's own row sits at position L - 1
+                ar.clear_slot(s_)
+                ar.advance(s_, L - 1)
         all_layers()
-    ctx.use_torch_stream()
-    for _ in range(3):
-        g.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1e3 / (reps * U * n_layers)
+        torch.cuda.synchronize()
+        if eager:
+            for _ in range(reps):
+                all_layers()
+            torch.cuda.synchronize()
+            continue
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ctx.use_torch_stream()
+            all_layers()
+        ctx.use_torch_stream()
+        us = _replay_time_us(g, reps, U * n_layers)
+        cfg = W.SelfDecode(base.name, base.beams, base.n_heads, L)
+        gbs = cfg.bytes() / (us * 1e-6) / 1e9
+        res[L] = {"us_per_launch": round(us, 3), "GBps": round(gbs, 1),
+                  "bytes_per_launch": cfg.bytes(), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"decode self L={L}: {us:.3f} us/launch, {gbs:.1f} GB/s")
     for ar in arenas:
         ar.close()
-    return cfg, us, cfg.bytes() / (us * 1e-6) / 1e9
+    return res
 
 
 def bench_capture(wrs, W, ctx, reps, use_graph=True):
@@ -245,7 +382,7 @@ def bench_capture(wrs, W, ctx, reps, use_graph=True):
     return cfg, us, gbs
 
 
-def bench_linear(wrs, cfg, ctx, reps):
+def bench_linear(wrs, cfg, ctx, reps, settle=True):
     """One fused QKV projection per step, inputs resident; bf16 rows out."""
     import torch
     x = torch.from_numpy(cfg.x()).cuda()
@@ -254,7 +391,9 @@ def bench_linear(wrs, cfg, ctx, reps):
     w = torch.from_numpy(cfg.w()).cuda()
     b = torch.from_numpy(cfg.bias()).cuda()
     out = torch.empty((cfg.n_tokens, cfg.n_out), dtype=torch.bfloat16, device="cuda")
-    for _ in range(150):  # ~50 ms of work: the clocks settle first
+    if settle:
+        settle_clocks(lambda: wrs.linear(x, w, b, out, ctx=ctx), 0.5)
+    else:
         wrs.linear(x, w, b, out, ctx=ctx)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -268,9 +407,10 @@ def bench_linear(wrs, cfg, ctx, reps):
     return ms, cfg.flops() / (ms * 1e-3) / 1e12
 
 
-def bench_weight_stream(wrs, W, ctx, reps):
+def bench_weight_stream(wrs, W, ctx, reps, eager=False):
     """One decoder step's projections for 5 beams, replayed from a HIP graph:
-    every launch streams its f16 weights once (the decode-sized linear path)."""
+    every launch streams its f16 weights once (the decode-sized linear path).
+    `eager` runs `reps` plain steps and returns (counter passes)."""
     import torch
     cfg = W.LARGE_DECODE_WEIGHTS
     gen = torch.Generator(device="cuda").manual_seed(0x5EED)
@@ -309,6 +449,11 @@ def bench_weight_stream(wrs, W, ctx, reps):
 
     step()
     torch.cuda.synchronize()
+    if eager:
+        for _ in range(reps):
+            step()
+        torch.cuda.synchronize()
+        return cfg, len(calls)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         ctx.use_torch_stream()
@@ -511,22 +656,39 @@ def calibration_copy():
     torch.cuda.synchronize()
 
 
-def measure_traffic(only: str, kernel_tag: str, extra: list[str]):
-    """HBM bytes per call of the kernel(s) whose name contains kernel_tag.
+# kernel-name patterns of each leg in the counter passes (demangled names)
+TRAFFIC_LEGS = {
+    "encoder": (r"fa2_prefill_d64<__bf16>", None),
+    "encoder_base": (r"fa2_prefill_d64<_Float16>", None),
+    "decode": (r"decode_f16<\s*5\s*,", None),
+    "decode_self": (r"decode_f16<\s*1\s*,", None),
+    "capture": (r"capture_cross", None),
+    "linear": (r"linear_f16w", None),
+    "stream": (r"gemv_f16w", "per_step"),
+}
+
+
+def measure_traffic(extra: list[str]):
+    """HBM bytes per call of every leg's kernel(s).
 
     Two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch)
-    over `bench.py --only <only>`; each counter is scaled by what it reads for
-    the plain copy of CALIB_BYTES in the same run. Returns None when rocprofv3
-    is unavailable or a pass fails.
+    over `bench.py --only traffic`, which runs every leg eagerly a few times;
+    each counter is scaled by what it reads for the plain device copy of
+    CALIB_BYTES in the same run. Returns {leg: {...}} (legs whose kernels are
+    missing are left out), or None when rocprofv3 is unavailable or a pass
+    fails.
     """
+    import re
     if shutil.which("rocprofv3") is None:
         return None
-    out = {}
+    res = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         with tempfile.TemporaryDirectory(dir="/tmp") as d:
-            cmd = ["timeout", "-s", "KILL", "150", "rocprofv3", "--pmc", counter, "-d", d, "-o",
-                   "t", "--", sys.executable, str(Path(__file__).resolve()), "--only", only] + extra
+            cmd = ["timeout", "-s", "KILL", "300", "rocprofv3", "--pmc", counter, "-d", d, "-o",
+                   "t", "--", sys.executable, str(Path(__file__).resolve()), "--only",
+                   "traffic"] + extra
             env = dict(os.environ, TMPDIR="/tmp")
+            log(f"traffic: {counter} pass")
             r = subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, env=env,
                                cwd="/tmp")
             dbs = list(Path(d).rglob("*_results.db"))
@@ -534,65 +696,128 @@ def measure_traffic(only: str, kernel_tag: str, extra: list[str]):
                 log(f"traffic: {counter} pass failed (rc={r.returncode})")
                 return None
             db = sqlite3.connect(str(dbs[0]))
-            rows = db.execute("select kernel_name, avg(value), max(value) from counters_collection "
-                              "where counter_name = ? group by kernel_name", (counter,)).fetchall()
+            rows = db.execute("select kernel_name, avg(value), max(value), sum(value), count(*) "
+                              "from counters_collection where counter_name = ? "
+                              "group by kernel_name", (counter,)).fetchall()
             db.close()
-            kern = [v for n, v, _ in rows if kernel_tag in n]
             # the calibration copy is the largest dispatch of its kernel: other,
             # smaller copies (input set-up) can share the kernel's name
-            copy = [vmax for n, _, vmax in rows if "copy" in n.lower() or "elementwise" in n.lower()]
-            if not kern or not copy or max(copy) <= 0:
-                log(f"traffic: {counter}: kernels not found in the profile")
+            copy = [vmax for n, _, vmax, _, _ in rows
+                    if "copy" in n.lower() or "elementwise" in n.lower()]
+            if not copy or max(copy) <= 0:
+                log(f"traffic: {counter}: no calibration copy in the profile")
                 return None
             factor = CALIB_BYTES / (max(copy) * 1024.0)
-            # one call of the path = one dispatch of each matching kernel
-            # (the capture runs as two passes)
-            out[counter] = sum(kern) * 1024.0 * factor
-            out[counter + "_factor"] = factor
-            log(f"traffic: {only} {counter} = {sum(kern):.1f} KiB per call over {len(kern)} "
-                f"kernel(s), copy of {CALIB_BYTES} B reads {max(copy):.1f} KiB -> "
-                f"factor {factor:.4f}")
-    return out
+            for leg, (pat, mode) in TRAFFIC_LEGS.items():
+                hit = [(n, av, tot, cnt) for n, av, _, tot, cnt in rows if re.search(pat, n)]
+                if not hit:
+                    continue
+                if mode == "per_step":
+                    steps = TRAFFIC_STREAM_STEPS
+                    kib = sum(t for _, _, t, _ in hit) / steps
+                else:
+                    # one call = one dispatch of each matching kernel (the
+                    # capture runs as two passes)
+                    kib = sum(av for _, av, _, _ in hit)
+                res.setdefault(leg, {})[counter] = kib * 1024.0 * factor
+                res[leg][counter + "_factor"] = round(factor, 4)
+                log(f"traffic: {leg} {counter} = {kib:.1f} KiB per call over "
+                    f"{len(hit)} kernel(s); factor {factor:.4f}")
+    return {leg: v for leg, v in res.items() if "FETCH_SIZE" in v and "WRITE_SIZE" in v}
 
 
-def cpu_baseline_encoder(cfg, qkv, threads):
+TRAFFIC_STREAM_STEPS = 3
+
+
+def run_traffic_legs(wrs, W, ctx):
+    """Every leg a few times, eagerly, then the calibration copy: the program
+    the counter passes profile."""
+    bench_encoder(wrs, W, ctx, 3, 1, settle=False)
+    bench_encoder(wrs, W, ctx, 3, 1, cfg=W.BASE_ENCODER, settle=False)
+    bench_decode(wrs, W, ctx, 3, use_graph=False)
+    bench_decode_self(wrs, W, ctx, 3, lengths=(W.SMALL_SELF_DECODE.ctx,), eager=True)
+    bench_capture(wrs, W, ctx, 3, use_graph=False)
+    bench_linear(wrs, W.LARGE_QKV_F16, ctx, 3, settle=False)
+    bench_weight_stream(wrs, W, ctx, TRAFFIC_STREAM_STEPS, eager=True)
+    calibration_copy()
+
+
+def cpu_baseline_encoder(cfg, qkv, info):
+    """The oracle's tiled flash_attention_2 on one window, timed by the
+    reference's method (bench_flash_attention_tiled.rs:109-134, :240-249):
+    one warm call each, then best of 9 alternating with the materialized
+    baseline, on available_parallelism() threads."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as orc
     q, k, v = (np.ascontiguousarray(x[0].reshape(-1)) for x in qkv)
     out = np.zeros_like(q)
+    mat = np.zeros_like(q)
     T, H, dm = cfg.t, cfg.n_heads, cfg.d_model
-    best = float("inf")
-    t_end = time.time() + 20.0
-    reps = 0
-    while reps < 5 and (reps < 2 or time.time() < t_end):
-        t0 = time.perf_counter()
-        orc.flash_attention_2(q, k, v, T, T, H, dm, False, out, n_threads=threads)
-        best = min(best, time.perf_counter() - t0)
-        reps += 1
+    n = info["threads"]
+    tiled = lambda: orc.flash_attention_2(q, k, v, T, T, H, dm, False, out, n_threads=n)
+    base = lambda: orc.materialized_attention(q, k, v, T, T, H, dm, mat, n_threads=n)
+    tiled()
+    base()
+    t_tiled, t_mat = time_both(tiled, base)
     flops = 4.0 * H * T * T * 64
-    return {"value": flops / best / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"1 of 16 windows (20 heads x 1500 x 1500), best of {reps}, "
-                      f"{best * 1e3:.1f} ms"}
+    return {"value": round(flops / t_tiled / 1e12, 4), "unit": "TFLOP/s", "cores": n,
+            "kind": "port",
+            "materialized_value": round(flops / t_mat / 1e12, 4),
+            "cpu": info["model"], "nproc": info["nproc"], "cgroup_cpus": info["cgroup_cpus"],
+            "sample": f"1 of {cfg.batch} windows ({H} heads x {T} x {T}); the oracle's tiled "
+                      f"flash_attention_2 best of {REPS} alternating with its materialized "
+                      f"baseline (bench_flash_attention_tiled.rs method), "
+                      f"{t_tiled * 1e3:.1f} ms vs {t_mat * 1e3:.1f} ms"}
 
 
-def cpu_baseline_decode(cfg):
+def cpu_baseline_decode(cfg, info):
+    """One layer's cross-attention decode: single_token_mha_d64 for each beam in
+    turn over f32 K/V (the reference's serial per-slot loop,
+    decoder.rs:689-724), one thread, best of 9 after a warm call."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as orc
     kk, vv = cfg.kv(0)
     k, v = np.ascontiguousarray(kk.ravel()), np.ascontiguousarray(vv.ravel())
     q = cfg.q(0)
     out = np.zeros(cfg.d_model, np.float32)
-    best = float("inf")
-    for _ in range(5):
-        t0 = time.perf_counter()
-        for b in range(cfg.beams):  # the reference's per-slot loop (decoder.rs:689-724)
+
+    def layer():
+        for b in range(cfg.beams):
             orc.single_token_mha_d64(np.ascontiguousarray(q[b]), k, v, cfg.n_audio, cfg.n_heads,
                                      cfg.d_model, out)
-        best = min(best, time.perf_counter() - t0)
-    return {"value": cfg.bytes_per_layer() / best / 1e9, "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"1 layer, 5 beams read serially from f32 K/V, best of 5, "
-                      f"{best * 1e3:.2f} ms"}
+
+    layer()
+    best = time_best(layer)
+    return {"value": round(cfg.bytes_per_layer() / best / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port", "cpu": info["model"],
+            "sample": f"1 layer, {cfg.beams} beams read serially from f32 K/V, best of {REPS}, "
+                      f"{best * 1e3:.3f} ms"}
+
+
+def cpu_baseline_decode_self(W, L, info):
+    """One layer's self-attention decode at valid length L: the reference's
+    per-slot loop (decoder.rs:617-647) calling single_token_mha_d64 over each
+    slot's f32 cache of L rows (decoder.rs:852-855), one thread."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    cfg = W.SelfDecode(W.SMALL_SELF_DECODE.name, W.SMALL_SELF_DECODE.beams,
+                       W.SMALL_SELF_DECODE.n_heads, L)
+    kvs = [tuple(np.ascontiguousarray(x.ravel()) for x in cfg.kv(s)) for s in range(cfg.beams)]
+    q = cfg.q()
+    out = np.zeros(cfg.d_model, np.float32)
+
+    def layer():
+        for s_ in range(cfg.beams):
+            k, v = kvs[s_]
+            orc.single_token_mha_d64(np.ascontiguousarray(q[s_]), k, v, L, cfg.n_heads,
+                                     cfg.d_model, out)
+
+    layer()
+    best = time_best(layer)
+    return {"value": round(cfg.bytes() / best / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port", "cpu": info["model"],
+            "sample": f"1 layer, {cfg.beams} slots x {L} rows read serially from f32 K/V, best "
+                      f"of {REPS}, {best * 1e6:.1f} us"}
 
 
 def cpu_baseline_capture(cfg):
@@ -603,16 +828,14 @@ def cpu_baseline_capture(cfg):
     k = np.ascontiguousarray(cfg.k(layer).ravel())
     sel = cfg.pairs(layer)
     out = np.zeros(cfg.n_tokens * len(cfg.heads) * cfg.n_audio, np.float32)
-    best = float("inf")
-    for _ in range(5):
-        t0 = time.perf_counter()
-        orc.capture_cross_attention_heads(q, k, cfg.n_tokens, cfg.n_audio, cfg.n_heads,
-                                          cfg.d_model, sel, len(cfg.heads), 0, out)
-        best = min(best, time.perf_counter() - t0)
-    return {"value": cfg.bytes_per_pair() / best / 1e9, "unit": "GB/s", "cores": 1,
+    run = lambda: orc.capture_cross_attention_heads(q, k, cfg.n_tokens, cfg.n_audio, cfg.n_heads,
+                                                    cfg.d_model, sel, len(cfg.heads), 0, out)
+    run()
+    best = time_best(run)
+    return {"value": round(cfg.bytes_per_pair() / best / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"1 layer's pair ({cfg.n_tokens} tokens x {cfg.n_audio} frames), best of 5, "
-                      f"{best * 1e3:.2f} ms"}
+            "sample": f"1 layer's pair ({cfg.n_tokens} tokens x {cfg.n_audio} frames), best of "
+                      f"{REPS}, {best * 1e3:.2f} ms"}
 
 
 def cpu_baseline_linear(cfg, threads):
@@ -624,14 +847,13 @@ def cpu_baseline_linear(cfg, threads):
     w = np.ascontiguousarray(cfg.w())
     b = cfg.bias()
     out = np.zeros(n * cfg.n_out, np.float32)
-    best = float("inf")
-    for _ in range(3):
-        t0 = time.perf_counter()
-        orc.f16_linear(w, cfg.n_out, cfg.n_in, x, b, n, out, n_threads=threads)
-        best = min(best, time.perf_counter() - t0)
+    run = lambda: orc.f16_linear(w, cfg.n_out, cfg.n_in, x, b, n, out, n_threads=threads)
+    run()
+    best = time_best(run)
     flops = 2.0 * n * cfg.n_in * cfg.n_out
-    return {"value": flops / best / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"1 window of 16 ({n} x {cfg.n_in} x {cfg.n_out}), best of 3, "
+    return {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"1 window of 16 ({n} x {cfg.n_in} x {cfg.n_out}), best of {REPS}, "
                       f"{best * 1e3:.1f} ms"}
 
 
@@ -647,30 +869,35 @@ def cpu_baseline_stream(cfg, threads):
     xs = {c: np.ascontiguousarray(rng.standard_normal((cfg.beams, c)).astype(np.float32).ravel())
           for _, c in mats}
     outs = {r: np.zeros(cfg.beams * r, np.float32) for r, _ in mats}
-    best = float("inf")
-    for _ in range(3):
-        t0 = time.perf_counter()
+    def run():
         for w in ws:
             r, c = w.shape
             orc.f16_linear(w, r, c, xs[c], None, cfg.beams, outs[r], n_threads=threads)
-        best = min(best, time.perf_counter() - t0)
+
+    run()
+    best = time_best(run)
     nbytes = sum(r * c * 2 for r, c in mats)
     return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"one layer's 8 projections ({nbytes / 1e6:.1f} MB of f16 weights, "
-                      f"{cfg.beams} rows), best of 3, {best * 1e3:.2f} ms"}
+                      f"{cfg.beams} rows), best of {REPS}, {best * 1e3:.2f} ms"}
+
+
+def _roof(achieved, peak, unit, bound, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # ~75 ms of untimed encoder steps: the clocks settle within about 300 steps
-    ap.add_argument("--warmup", type=int, default=300)
+    # untimed steps after the time-bounded clock-settle phase
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--eager", action="store_true",
-                    help="with --only decode: plain launches instead of a graph replay")
+                    help="with --only decode/decode_self/capture: plain launches, no graph")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 HBM-traffic passes")
     ap.add_argument("--capture-reps", type=int, default=100)
@@ -679,7 +906,8 @@ def main():
                     help="with --only linear: the f16-activation projection only")
     ap.add_argument("--stream-reps", type=int, default=20)
     ap.add_argument("--rows-reps", type=int, default=50)
-    ap.add_argument("--only", choices=["encoder", "decode", "capture", "linear", "stream", "rows"],
+    ap.add_argument("--only", choices=["encoder", "encoder_base", "decode", "decode_self",
+                                       "capture", "linear", "stream", "rows", "traffic"],
                     default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
@@ -697,18 +925,24 @@ def main():
     ctx.use_torch_stream()
     props = torch.cuda.get_device_properties(0)
 
-    if args.only == "encoder":
-        _, ms, tflops, _ = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
+    if args.only == "traffic":
+        run_traffic_legs(wrs, W, ctx)
+        return
+    if args.only in ("encoder", "encoder_base"):
+        cfg = W.LARGE_ENCODER if args.only == "encoder" else W.BASE_ENCODER
+        _, ms, tflops, _, n = bench_encoder(wrs, W, ctx, args.steps, args.warmup, cfg=cfg)
         calibration_copy()
-        log(f"encoder only: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s")
+        log(f"{args.only} only: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s (settle {n} launches)")
         return
     if args.only == "decode":
-        _, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps, use_graph=not args.eager)
+        _, us, gbs, floor = bench_decode(wrs, W, ctx, args.decode_reps, use_graph=not args.eager)
         calibration_copy()
-        log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s")
-        if not args.eager:
-            _, sus, sgbs_ = bench_decode_self(wrs, W, ctx, args.decode_reps)
-            log(f"decode self (whisper-small, length 224): {sus:.3f} us/launch, {sgbs_:.1f} GB/s")
+        log(f"decode only: {us:.3f} us/launch, {gbs:.1f} GB/s; floor {floor}")
+        return
+    if args.only == "decode_self":
+        res = bench_decode_self(wrs, W, ctx, args.decode_reps, eager=args.eager)
+        calibration_copy()
+        log(f"decode self only: {res}")
         return
     if args.only == "linear":
         cfgs = (W.LARGE_QKV_F16,) if args.linear_f16_only else (W.LARGE_QKV_F16, W.LARGE_QKV_F32)
@@ -732,9 +966,12 @@ def main():
         calibration_copy()
         log(f"capture only: {cus:.3f} us/launch, {cgbs:.1f} GB/s")
         return
-    cfg, ms, tflops, qkv = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
-    dcfg, us, gbs = bench_decode(wrs, W, ctx, args.decode_reps)
-    dscfg, dsus, dsgbs = bench_decode_self(wrs, W, ctx, args.decode_reps)
+
+    cfg, ms, tflops, qkv, settled = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
+    bcfg, bms, btflops, bqkv, bsettled = bench_encoder(wrs, W, ctx, args.steps, args.warmup,
+                                                       cfg=W.BASE_ENCODER)
+    dcfg, us, gbs, floor = bench_decode(wrs, W, ctx, args.decode_reps)
+    sweep = bench_decode_self(wrs, W, ctx, args.decode_reps)
     ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
     lcfg = W.LARGE_QKV_F16
     lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
@@ -745,33 +982,35 @@ def main():
     host_slice = bench_host_slice(wrs, W, ctx)
     copy_gbs = copy_bandwidth()
 
-    enc_traffic = dec_traffic = cap_traffic = lin_traffic = None
+    traffic = None
     if not args.no_traffic:
         log("traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes")
-        enc_traffic = measure_traffic("encoder", "fa2_prefill", ["--steps", "3", "--warmup", "1"])
-        dec_traffic = measure_traffic("decode", "decode_f16", ["--decode-reps", "3", "--eager"])
-        cap_traffic = measure_traffic("capture", "capture_cross", ["--capture-reps", "3",
-                                                                    "--eager"])
-        lin_traffic = measure_traffic("linear", "linear_f16w",
-                                      ["--linear-reps", "3", "--linear-f16-only"])
+        traffic = measure_traffic([])
 
-    def traffic_bytes(t):
-        return None if t is None else round(t["FETCH_SIZE"] + t["WRITE_SIZE"])
+    def traffic_bytes(leg):
+        if not traffic or leg not in traffic:
+            return None
+        return round(traffic[leg]["FETCH_SIZE"] + traffic[leg]["WRITE_SIZE"])
 
-    threads = min(16, os.cpu_count() or 1)
-    cpu_enc = cpu_dec = cpu_cap = cpu_lin = cpu_stream = None
+    info = cpu_info()
+    n = info["threads"]
+    cpu = {}
     if not args.no_cpu:
-        log(f"cpu baseline: oracle encoder window on {threads} threads")
-        cpu_enc = cpu_baseline_encoder(cfg, qkv, threads)
-        log("cpu baseline: oracle decode layer, 1 thread")
-        cpu_dec = cpu_baseline_decode(dcfg)
+        log(f"cpu baseline: oracle encoder windows on {n} threads ({info['model']})")
+        cpu["encoder"] = cpu_baseline_encoder(cfg, qkv, info)
+        cpu["encoder_base"] = cpu_baseline_encoder(bcfg, bqkv, info)
+        log("cpu baseline: oracle decode layers, 1 thread")
+        cpu["decode"] = cpu_baseline_decode(dcfg, info)
+        cpu["decode_self"] = cpu_baseline_decode_self(W, W.SMALL_SELF_DECODE.ctx, info)
         log("cpu baseline: oracle capture of one layer, 1 thread")
-        cpu_cap = cpu_baseline_capture(ccfg)
-        log(f"cpu baseline: oracle f16_linear, one window, {threads} threads")
-        cpu_lin = cpu_baseline_linear(lcfg, threads)
-        log(f"cpu baseline: oracle f16_linear, one decoder layer's projections, {threads} threads")
-        cpu_stream = cpu_baseline_stream(scfg, threads)
+        cpu["capture"] = cpu_baseline_capture(ccfg)
+        log(f"cpu baseline: oracle f16_linear, one window, {n} threads")
+        cpu["linear"] = cpu_baseline_linear(lcfg, n)
+        log(f"cpu baseline: oracle f16_linear, one decoder layer's projections, {n} threads")
+        cpu["stream"] = cpu_baseline_stream(scfg, n)
 
+    L0 = W.SMALL_SELF_DECODE.ctx
+    self_ref = sweep[L0]
     line = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -786,62 +1025,69 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": cfg.name, "windows": cfg.batch, "heads": cfg.n_heads,
-                   "frames": cfg.t, "d_head": 64, "flops_per_step": cfg.flops()},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_bytes(enc_traffic)},
-        "cpu_baseline": cpu_enc,
+                   "frames": cfg.t, "d_head": 64, "flops_per_step": cfg.flops(),
+                   "clock_settle": {"seconds": SETTLE_SECONDS, "launches": settled,
+                                    "then_warmup_steps": args.warmup}},
+        "roofline": _roof(tflops, PEAK_BF16_TFLOPS, "TFLOP/s", "mfma", traffic_bytes("encoder")),
+        "cpu_baseline": cpu.get("encoder"),
+        "encoder_base": {
+            "workload": bcfg.name, "value": round(btflops, 2), "unit": "TFLOP/s",
+            "ms_per_step": round(bms, 4), "flops_per_step": bcfg.flops(), "dtype": "f16",
+            "clock_settle_launches": bsettled,
+            "roofline": _roof(btflops, PEAK_BF16_TFLOPS, "TFLOP/s", "mfma",
+                              traffic_bytes("encoder_base")),
+            "cpu_baseline": cpu.get("encoder_base"),
+        },
         "decode_cross": {
             "workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s",
             "us_per_launch": round(us, 3), "launches_per_step": dcfg.n_layers,
             "bytes_per_launch": dcfg.bytes_per_layer(), "dtype": "f16",
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                         "traffic": traffic_bytes(dec_traffic)},
-            "cpu_baseline": cpu_dec,
+            "roofline": _roof(gbs, PEAK_HBM_GBS, "GB/s", "hbm", traffic_bytes("decode")),
+            "single_launch_read_floor": floor,
+            "frac_of_read_floor": round(floor["us_per_launch"] / us, 4) if floor else None,
+            "cpu_baseline": cpu.get("decode"),
         },
         "decode_self": {
-            "workload": dscfg.name + f", valid length {dscfg.ctx} of {dscfg.max_ctx}",
-            "value": round(dsgbs, 1), "unit": "GB/s", "us_per_launch": round(dsus, 3),
-            "launches_per_step": 12, "bytes_per_launch": dscfg.bytes(), "dtype": "f16",
-            "roofline": {"bound": "hbm", "achieved": round(dsgbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(dsgbs / PEAK_HBM_GBS, 4),
-                         "traffic": None},
+            "workload": W.SMALL_SELF_DECODE.name + f", valid length {L0} of "
+                                                   f"{W.SMALL_SELF_DECODE.max_ctx}",
+            "value": self_ref["GBps"], "unit": "GB/s", "us_per_launch": self_ref["us_per_launch"],
+            "launches_per_step": 12, "bytes_per_launch": self_ref["bytes_per_launch"],
+            "dtype": "f16",
+            "roofline": _roof(self_ref["GBps"], PEAK_HBM_GBS, "GB/s", "hbm",
+                              traffic_bytes("decode_self")),
+            "sweep": {str(L): v for L, v in sweep.items()},
+            "cpu_baseline": cpu.get("decode_self"),
         },
         "capture": {
             "workload": ccfg.name, "value": round(cgbs, 1), "unit": "GB/s",
             "us_per_launch": round(cus, 3), "launches_per_step": len(ccfg.layers()),
             "bytes_per_launch": ccfg.bytes_per_pair(), "dtype": "f32",
-            "roofline": {"bound": "hbm", "achieved": round(cgbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(cgbs / PEAK_HBM_GBS, 4),
-                         "traffic": traffic_bytes(cap_traffic)},
-            "cpu_baseline": cpu_cap,
+            "roofline": _roof(cgbs, PEAK_HBM_GBS, "GB/s", "hbm", traffic_bytes("capture")),
+            "cpu_baseline": cpu.get("capture"),
         },
         "projection": {
             "workload": lcfg.name, "value": round(ltf, 2), "unit": "TFLOP/s",
             "ms_per_launch": round(lms, 4), "flops_per_launch": lcfg.flops(), "dtype": "f16",
-            "roofline": {"bound": "mfma", "achieved": round(ltf, 2), "peak": PEAK_BF16_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(ltf / PEAK_BF16_TFLOPS, 4),
-                         "traffic": traffic_bytes(lin_traffic)},
+            "roofline": _roof(ltf, PEAK_BF16_TFLOPS, "TFLOP/s", "mfma", traffic_bytes("linear")),
             "f32_exact": {"workload": W.LARGE_QKV_F32.name, "value": round(ltf32, 2),
                           "unit": "TFLOP/s", "ms_per_launch": round(lms32, 4)},
-            "cpu_baseline": cpu_lin,
+            "cpu_baseline": cpu.get("linear"),
         },
         "decoder_weight_stream": {
             "workload": scfg.name, "value": round(sgbs, 1), "unit": "GB/s",
             "ms_per_step": round(sms, 4), "launches_per_step": scfg.launches(),
             "weight_bytes_per_step": scfg.weight_bytes(), "dtype": "f16",
-            "roofline": {"bound": "hbm", "achieved": round(sgbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(sgbs / PEAK_HBM_GBS, 4), "traffic": None},
+            "roofline": _roof(sgbs, PEAK_HBM_GBS, "GB/s", "hbm", traffic_bytes("stream")),
             "vocabulary_projection": {"us": round(vms * 1e3, 2), "GBps": round(vgbs, 1),
                                       "frac_hbm": round(vgbs / PEAK_HBM_GBS, 4)},
             "with_layer_norms_and_gelu": snorms,
-            "cpu_baseline": cpu_stream,
+            "cpu_baseline": cpu.get("stream"),
         },
         "row_kernels": rows,
         "host_slice": host_slice,
         "device": {"name": props.name, "cu": props.multi_processor_count,
                    "copy_GBps": round(copy_gbs, 1)},
+        "host": info,
     }
     print(json.dumps(line), flush=True)
 

@@ -32,6 +32,7 @@ extern "C" {
 #define WRS_EHIP (-3)        /* HIP runtime error; see wrs_attn_last_error */
 #define WRS_EUNSUPPORTED (-4) /* valid for the reference, not handled on the GPU */
 #define WRS_ERANGE (-5)      /* layer/slot index or length outside the arena */
+#define WRS_ECAPTURE (-6)    /* context scratch would grow while the stream records a graph */
 
 /* Element types of device-resident tensors. */
 #define WRS_F32 0
@@ -65,6 +66,26 @@ int wrs_attn_synchronize(wrs_attn_ctx *ctx);
 /* Text of the last error on this context (valid until the next call). */
 const char *wrs_attn_last_error(wrs_attn_ctx *ctx);
 const char *wrs_attn_status_string(int status);
+
+/* Largest calls the context will serve, so that its scratch (split-K
+ * partials, capture statistics, split f32 projection rows) is allocated now
+ * rather than on the first call that needs it. No reference counterpart (the
+ * reference allocates per call on the host). Device-resident entry points
+ * never allocate once their sizes are reserved; a call that would grow
+ * scratch while the context's stream records a graph fails with
+ * WRS_ECAPTURE instead. Switching streams (wrs_attn_set_stream) drains the
+ * old stream unless either stream is recording a graph. Zero fields are
+ * ignored; reserving never shrinks. Synchronous. */
+typedef struct wrs_reserve {
+    size_t n_heads;        /* heads of the planes decode and capture read */
+    size_t decode_rows;    /* query rows of one decode call: slots or beams */
+    size_t decode_keys;    /* longest cache one decode call reads */
+    size_t capture_tokens; /* query rows of one alignment-head capture */
+    size_t capture_keys;   /* n_audio of the captured cross plane */
+    size_t linear_tokens;  /* rows of one f32-input projection (above 8) */
+    size_t linear_n_in;    /* its input width */
+} wrs_reserve;
+int wrs_attn_reserve(wrs_attn_ctx *ctx, const wrs_reserve *r);
 
 /* ---- host-slice drop-ins (synchronous; f32 host buffers) ---------------
  * Same arguments, argument meaning and results as the reference functions,
@@ -154,7 +175,9 @@ int wrs_kv_advance(wrs_kv *kv, size_t slot, size_t n);
  * K and V of one layer, converted to f16 head planes. */
 int wrs_kv_set_cross(wrs_kv *kv, size_t layer, const float *k, const float *v, size_t n_audio,
                      int src_on_host);
-int wrs_kv_cross_len(wrs_kv *kv, size_t *n_audio);
+/* n_audio of one layer's stored cross K/V (DecoderKvCache keeps cross K/V per
+ * layer, decoder.rs:136-139); 0 after wrs_kv_invalidate_cross. */
+int wrs_kv_cross_len(wrs_kv *kv, size_t layer, size_t *n_audio);
 /* Raw device pointers of the arena planes (for tests and fused callers). */
 int wrs_kv_self_planes(wrs_kv *kv, void **k, void **v, size_t *slot_stride_elems);
 int wrs_kv_cross_planes(wrs_kv *kv, void **k, void **v);
@@ -169,7 +192,9 @@ int wrs_attn_decode_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const size
                          size_t n, const float *q, float *out);
 /* Cross-attention step: decoder.rs:689-724 -> multi_head_attention ->
  * single_token_mha_d64 (attention.rs:102-105), all n_beams query rows of one
- * utterance against the shared cross plane in one launch (K/V read once). */
+ * utterance against the shared cross plane in one launch (K/V read once).
+ * A layer without cross K/V (never set, invalidated, or an arena created with
+ * n_audio_max = 0) gives zero rows, as t_kv == 0 does (attention.rs:93-96). */
 int wrs_attn_decode_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
                           size_t n_beams, float *out);
 /* Multi-token rows (prompt prefill): decoder.rs:857-891 self-attention with
@@ -268,6 +293,16 @@ int wrs_gelu_inplace(wrs_attn_ctx *ctx, float *data, size_t n);
 int wrs_kv_set_cross_proj(wrs_kv *kv, int x_dtype, const void *enc, size_t enc_len,
                           int64_t enc_row_stride, size_t n_audio, const void *const *w_k,
                           const void *const *w_v, const float *const *b_v);
+
+/* ---- measurement helper ----------------------------------------------------
+ * No reference counterpart: reads `bytes` of device memory (16-byte aligned,
+ * a multiple of 16) once, in one launch shaped like the split-K decode's grid
+ * (512 threads x 64 bytes per workgroup), and writes one float per workgroup
+ * to sink (sink_len >= ceil(bytes / 32768)). It measures the practical floor
+ * of a decode-sized launch (launch, ramp and DRAM latency included).
+ * Asynchronous. */
+int wrs_stream_read(wrs_attn_ctx *ctx, const void *src, size_t bytes, float *sink,
+                    size_t sink_len);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,9 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, ctypes.c_int, _f32p,
                            ctypes.c_int]
             fn.restype = ctypes.c_int
+        L.wrs_oracle_materialized_attention.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz,
+                                                        _f32p, ctypes.c_int]
+        L.wrs_oracle_materialized_attention.restype = ctypes.c_int
         L.wrs_oracle_single_token_mha_d64.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]
         L.wrs_oracle_single_token_mha_d64.restype = ctypes.c_int
         L.wrs_oracle_mha_with_cache.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
@@ -134,6 +137,18 @@ def flash_attention_2(q, k, v, t_q, t_kv, n_heads, d_model, causal, output, n_th
                                             d_model, int(bool(causal)), _ptr(output),
                                             _threads(n_threads))
     _check(rc, "flash_attention_2")
+
+
+def materialized_attention(q, k, v, t_q, t_kv, n_heads, d_model, output, n_threads=None):
+    """crates/tensor/tests/bench_flash_attention_tiled.rs:46-107: full score
+    matrix per head, softmax_inplace per row, then scores x V (the reference's
+    benchmark baseline)."""
+    assert n_heads > 0 and d_model % n_heads == 0
+    assert q.size == t_q * d_model and k.size == t_kv * d_model
+    assert v.size == t_kv * d_model and output.size == t_q * d_model
+    rc = lib().wrs_oracle_materialized_attention(_ptr(q), _ptr(k), _ptr(v), t_q, t_kv, n_heads,
+                                                 d_model, _ptr(output), _threads(n_threads))
+    _check(rc, "materialized_attention")
 
 
 def multi_head_attention(q, k, v, t_q, t_kv, n_heads, d_model, causal, output, n_threads=None):

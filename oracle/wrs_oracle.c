@@ -460,6 +460,60 @@ int wrs_oracle_multi_head_attention(const float *q, const float *k,
 }
 
 /* ------------------------------------------------------------------------ */
+/* crates/tensor/tests/bench_flash_attention_tiled.rs:46-107                 */
+/* materialized_attention: the implementation the tiled kernel replaced and  */
+/* the reference's own timing baseline. Per head (parallel over heads, as    */
+/* into_par_iter): S = scale * (Q K^T) into a t_q x t_kv buffer (sgemm with   */
+/* alpha = scale: the dot product, then the scale), softmax_inplace per row,  */
+/* then O = S V. No causal mask, no t_kv == 0 special case (the benchmark    */
+/* shapes have neither).                                                     */
+/* ------------------------------------------------------------------------ */
+int wrs_oracle_materialized_attention(const float *q, const float *k, const float *v,
+                                      size_t t_q, size_t t_kv, size_t n_heads,
+                                      size_t d_model, float *out, int n_threads) {
+    if (n_heads == 0 || d_model % n_heads != 0) return -1;
+    const size_t d_head = d_model / n_heads;
+    const float scale = 1.0f / sqrtf((float)d_head);
+    int err = 0;
+#ifdef _OPENMP
+    int nt = n_threads > 0 ? n_threads : omp_get_num_procs();
+#pragma omp parallel for num_threads(nt) schedule(dynamic, 1)
+#endif
+    for (size_t h = 0; h < n_heads; ++h) {
+        const size_t ho = h * d_head;
+        float *scores = (float *)malloc(sizeof(float) * (t_q * t_kv ? t_q * t_kv : 1));
+        if (!scores) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+            err = -12;
+            continue;
+        }
+        for (size_t i = 0; i < t_q; ++i) {
+            const float *qi = q + i * d_model + ho;
+            for (size_t j = 0; j < t_kv; ++j) {
+                const float *kj = k + j * d_model + ho;
+                float acc = 0.0f;
+                for (size_t d = 0; d < d_head; ++d) acc = fmaf(qi[d], kj[d], acc);
+                scores[i * t_kv + j] = scale * acc;
+            }
+            wrs_oracle_softmax_inplace(scores + i * t_kv, t_kv);
+        }
+        for (size_t i = 0; i < t_q; ++i) {
+            float *oi = out + i * d_model + ho;
+            for (size_t d = 0; d < d_head; ++d) oi[d] = 0.0f;
+            for (size_t j = 0; j < t_kv; ++j) {
+                const float w = scores[i * t_kv + j];
+                const float *vj = v + j * d_model + ho;
+                for (size_t d = 0; d < d_head; ++d) oi[d] = fmaf(w, vj[d], oi[d]);
+            }
+        }
+        free(scores);
+    }
+    return err;
+}
+
+/* ------------------------------------------------------------------------ */
 /* decoder.rs:835-892 multi_head_attention_with_cache                        */
 /* ------------------------------------------------------------------------ */
 int wrs_oracle_mha_with_cache(const float *q, const float *k, const float *v,

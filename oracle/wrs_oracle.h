@@ -46,6 +46,12 @@ int wrs_oracle_multi_head_attention(const float *q, const float *k,
                                     float *out, int n_threads);
 
 /* crates/tensor/src/ops/attention.rs:246-434 (one query per head, d_head 64) */
+/* bench_flash_attention_tiled.rs:46-107: the materialized (full score
+ * matrix per head) attention the reference benchmarks the tiled kernel
+ * against. */
+int wrs_oracle_materialized_attention(const float *q, const float *k, const float *v,
+                                      size_t t_q, size_t t_kv, size_t n_heads,
+                                      size_t d_model, float *out, int n_threads);
 int wrs_oracle_single_token_mha_d64(const float *q, const float *k,
                                     const float *v, size_t t_kv,
                                     size_t n_heads, size_t d_model, float *out);

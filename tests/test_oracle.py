@@ -140,6 +140,25 @@ def test_bench_shapes(orc, t_q, t_kv):
     assert np.abs(out.reshape(t_q, d_model) - ref).max() <= 1e-4
 
 
+@pytest.mark.parametrize("t_q,t_kv", [(1500, 1500), (64, 1500), (4096, 4096)])
+def test_materialized_baseline_matches_tiled(orc, t_q, t_kv):
+    # bench_flash_attention_tiled.rs:142-147 and :258-260: the tiled kernel and
+    # the materialized baseline agree within 1e-4 on every benchmark shape
+    # (6 heads, d_head 64, one xorshift stream seeded 0x5eed_1234 for q, k, v).
+    n_heads, d_head = 6, 64
+    d_model = n_heads * d_head
+    rng = orc.Rng(0x5EED_1234)
+    q, k, v = rng.fill(t_q * d_model), rng.fill(t_kv * d_model), rng.fill(t_kv * d_model)
+    tiled = np.zeros(t_q * d_model, np.float32)
+    mat = np.zeros(t_q * d_model, np.float32)
+    orc.flash_attention_2(q, k, v, t_q, t_kv, n_heads, d_model, False, tiled)
+    orc.materialized_attention(q, k, v, t_q, t_kv, n_heads, d_model, mat)
+    assert np.abs(tiled - mat).max() <= 1e-4
+    if t_q * t_kv <= 1500 * 1500:
+        ref = attention_f64(q, k, v, t_q, t_kv, n_heads, d_model).ravel()
+        assert np.abs(mat - ref).max() <= 1e-5
+
+
 # ---- edge cases fixed by attention.rs itself -------------------------------
 
 def test_t_q_zero_is_noop(orc):

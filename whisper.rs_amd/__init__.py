@@ -85,6 +85,13 @@ class Context:
     def synchronize(self) -> None:
         self.check(self._lib.wrs_attn_synchronize(self.handle), "wrs_attn_synchronize")
 
+    def reserve(self, **sizes) -> None:
+        """Size the context scratch for the largest calls it will serve
+        (``wrs_attn_reserve``): n_heads, decode_rows, decode_keys,
+        capture_tokens, capture_keys, linear_tokens, linear_n_in."""
+        r = _L.Reserve(**{k: int(v) for k, v in sizes.items()})
+        self.check(self._lib.wrs_attn_reserve(self.handle, ctypes.byref(r)), "wrs_attn_reserve")
+
 
 _default = None
 _default_lock = threading.Lock()
@@ -389,9 +396,10 @@ class KvArena:
         self._c(self._lib.wrs_kv_set_cross(self.handle, layer, pk, pv, nk // self.d_model, host),
                 "set_cross")
 
-    def cross_len(self) -> int:
+    def cross_len(self, layer: int = 0) -> int:
+        """n_audio of one layer's cross K/V (0 when not set or invalidated)."""
         n = ctypes.c_size_t()
-        self._c(self._lib.wrs_kv_cross_len(self.handle, ctypes.byref(n)), "cross_len")
+        self._c(self._lib.wrs_kv_cross_len(self.handle, layer, ctypes.byref(n)), "cross_len")
         return n.value
 
     def plane_pointers(self):

@@ -19,10 +19,19 @@ WRS_ENOMEM = -2
 WRS_EHIP = -3
 WRS_EUNSUPPORTED = -4
 WRS_ERANGE = -5
+WRS_ECAPTURE = -6
 
 WRS_F32 = 0
 WRS_F16 = 1
 WRS_BF16 = 2
+
+
+class Reserve(ctypes.Structure):
+    """wrs_reserve: the largest calls a context serves (scratch sized up front)."""
+
+    _fields_ = [(n, ctypes.c_size_t) for n in (
+        "n_heads", "decode_rows", "decode_keys", "capture_tokens", "capture_keys",
+        "linear_tokens", "linear_n_in")]
 
 
 class Layout(ctypes.Structure):
@@ -46,6 +55,8 @@ _SIGNATURES = {
     "wrs_attn_synchronize": (_int, [_vp]),
     "wrs_attn_last_error": (ctypes.c_char_p, [_vp]),
     "wrs_attn_status_string": (ctypes.c_char_p, [_int]),
+    "wrs_attn_reserve": (_int, [_vp, ctypes.POINTER(Reserve)]),
+    "wrs_stream_read": (_int, [_vp, _vp, _sz, _vp, _sz]),
     "wrs_flash_attention_2": (_int, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz, _int,
                                      _vp, _sz]),
     "wrs_multi_head_attention": (_int, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
@@ -69,7 +80,7 @@ _SIGNATURES = {
     "wrs_kv_append": (_int, [_vp, _sz, _sz, _vp, _vp, _sz, _int]),
     "wrs_kv_advance": (_int, [_vp, _sz, _sz]),
     "wrs_kv_set_cross": (_int, [_vp, _sz, _vp, _vp, _sz, _int]),
-    "wrs_kv_cross_len": (_int, [_vp, _szp]),
+    "wrs_kv_cross_len": (_int, [_vp, _sz, _szp]),
     "wrs_kv_self_planes": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _szp]),
     "wrs_kv_cross_planes": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
     "wrs_attn_decode_self": (_int, [_vp, _vp, _sz, _szp, _sz, _vp, _vp]),

@@ -121,19 +121,22 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   // Lane (col, kg) carries key kbase + col: d 8kg..8kg+7 and 32+8kg.. of its
   // K and V rows (the A-operand layout of a 16x16x32 MFMA).
   const int kbase = split * kChunk + wave * 16;
+  // Lanes past the visible length load nothing (their K and V stay zero), so
+  // an empty plane is never dereferenced.
   const bool valid = kbase + col < len;
-  const int64_t off = a.goff[g] + h * a.kv_hs + static_cast<int64_t>(valid ? kbase + col : 0) * 64 + 8 * kg;
-  const u32x4 kx0 = *reinterpret_cast<const u32x4*>(a.k + off);
-  const u32x4 kx1 = *reinterpret_cast<const u32x4*>(a.k + off + 32);
-  u32x4 vx0 = *reinterpret_cast<const u32x4*>(a.v + off);
-  u32x4 vx1 = *reinterpret_cast<const u32x4*>(a.v + off + 32);
+  const u32x4 zero4 = {0, 0, 0, 0};
+  u32x4 kx0 = zero4, kx1 = zero4, vx0 = zero4, vx1 = zero4;
+  if (valid) {
+    const int64_t off = a.goff[g] + h * a.kv_hs + static_cast<int64_t>(kbase + col) * 64 + 8 * kg;
+    kx0 = *reinterpret_cast<const u32x4*>(a.k + off);
+    kx1 = *reinterpret_cast<const u32x4*>(a.k + off + 32);
+    vx0 = *reinterpret_cast<const u32x4*>(a.v + off);
+    vx1 = *reinterpret_cast<const u32x4*>(a.v + off + 32);
+  }
   // Every load above is issued before any of them is waited on: the q
   // arithmetic below depends on a value defined after them.
   float one;
   __asm__ volatile("v_mov_b32 %0, 1.0" : "=v"(one) : : "memory");
-  const u32x4 zero4 = {0, 0, 0, 0};
-  vx0 = valid ? vx0 : zero4;
-  vx1 = valid ? vx1 : zero4;
 
   // q * scale * log2(e), scaled by 2^sh so the row max lies in [2^14, 2^15),
   // split into f16 high (columns 0-7 of B) and low (columns 8-15) parts.
@@ -355,7 +358,44 @@ __global__ __launch_bounds__(kThreads) void decode_exact_f32(ExactArgs a) {
   }
 }
 
+// Streaming read with the decode grid's shape: 512 threads x 64 bytes per
+// workgroup, every load issued before any is used; one float per workgroup
+// keeps the loads live.
+__global__ __launch_bounds__(512) void stream_read(const u32x4* src, int64_t n16, float* sink) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * 2048 + threadIdx.x;
+  u32x4 x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t idx = base + 512 * i;
+    x[i] = idx < n16 ? src[idx] : u32x4{0, 0, 0, 0};
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc ^= x[i].x ^ x[i].y ^ x[i].z ^ x[i].w;
+  __shared__ uint32_t red[8];
+  for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+    for (int w = 0; w < 8; ++w) r ^= red[w];
+    sink[blockIdx.x] = __builtin_bit_cast(float, r & 0x3fffffffu);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_stream_read(const void* src, int64_t bytes, float* sink, hipStream_t s) {
+  const int64_t n16 = bytes / 16;
+  const int64_t blocks = (n16 + 2047) / 2048;
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(stream_read, dim3(static_cast<unsigned>(blocks)), dim3(512), 0, s,
+                     static_cast<const u32x4*>(src), n16, sink);
+  return hipGetLastError();
+}
+
+int64_t stream_read_blocks(int64_t bytes) { return (bytes / 16 + 2047) / 2048; }
 
 size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows) {
   return static_cast<size_t>(n_groups) * n_heads * n_splits * rows * kPart;

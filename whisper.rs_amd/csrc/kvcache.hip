@@ -64,7 +64,49 @@ __global__ __launch_bounds__(256) void kv_copy_planes(const _Float16* src, _Floa
   for (int i = threadIdx.x; i < n; i += 256) d[i] = s[i];
 }
 
+// Zero fill of a strided [batch][head][row][cols] f32 region (replaces
+// memset nodes, which must not be recorded into captured graphs): one thread
+// per value.
+__global__ __launch_bounds__(256) void fill_zero_rows(float* base, int64_t bs, int64_t hs,
+                                                      int64_t rs, int n_heads, int n_rows,
+                                                      int cols) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t per_batch = static_cast<int64_t>(n_heads) * n_rows * cols;
+  const int b = static_cast<int>(blockIdx.y);
+  if (t >= per_batch) return;
+  const int c = static_cast<int>(t % cols);
+  const int64_t hr = t / cols;
+  const int r = static_cast<int>(hr % n_rows);
+  const int h = static_cast<int>(hr / n_rows);
+  base[b * bs + h * hs + r * rs + c] = 0.f;
+}
+
+__global__ __launch_bounds__(256) void fill_zero_u32(unsigned* p, int64_t n) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < n) p[t] = 0u;
+}
+
 }  // namespace
+
+hipError_t launch_fill_zero_rows(float* base, int64_t bs, int64_t hs, int64_t rs, int batch,
+                                 int n_heads, int n_rows, int cols, hipStream_t s) {
+  if (batch <= 0 || n_heads <= 0 || n_rows <= 0 || cols <= 0) return hipSuccess;
+  if (batch > 65535) return hipErrorInvalidConfiguration;
+  const int64_t per_batch = static_cast<int64_t>(n_heads) * n_rows * cols;
+  const int64_t blocks = (per_batch + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(fill_zero_rows, dim3(static_cast<unsigned>(blocks), batch), dim3(256), 0, s,
+                     base, bs, hs, rs, n_heads, n_rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_zero_u32(unsigned* p, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(fill_zero_u32, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, p, n);
+  return hipGetLastError();
+}
 
 hipError_t launch_kv_write_rows(const float* src, int64_t src_rs, int n, int n_heads,
                                 _Float16* dst, int64_t dst_hs, int pos, hipStream_t s) {

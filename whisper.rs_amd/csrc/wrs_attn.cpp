@@ -86,8 +86,22 @@ int fail(wrs_attn_ctx* c, int code, const char* what, hipError_t e = hipSuccess)
     if (e_ != hipSuccess) return fail((c), WRS_EHIP, #expr, e_); \
   } while (0)
 
+// True while the context's stream records a graph: no allocation, free or
+// host synchronization may happen then.
+bool capturing(wrs_attn_ctx* c) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(c->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// Grows a scratch buffer to at least `bytes`. Refused while the stream is
+// capturing (a captured graph would keep the old pointer, and hipMalloc /
+// hipFree cannot be recorded): size scratch with wrs_attn_reserve first.
+// `zero` clears the new buffer with a fill kernel (never a memset node).
 int grow(wrs_attn_ctx* c, void** p, size_t* cap, size_t bytes, bool zero) {
   if (*cap >= bytes) return WRS_OK;
+  if (capturing(c))
+    return fail(c, WRS_ECAPTURE,
+                "context scratch would grow during stream capture: call wrs_attn_reserve first");
   size_t want = std::max(bytes, *cap * 2);
   if (*p) {
     // The buffer may still be read by work queued on the stream.
@@ -101,7 +115,9 @@ int grow(wrs_attn_ctx* c, void** p, size_t* cap, size_t bytes, bool zero) {
     return fail(c, WRS_ENOMEM, "hipMalloc of context scratch failed");
   }
   *cap = want;
-  if (zero) WRS_HIP(c, hipMemsetAsync(*p, 0, want, c->stream));
+  if (zero)
+    WRS_HIP(c, wrs::launch_fill_zero_u32(static_cast<unsigned*>(*p),
+                                         static_cast<int64_t>(want / sizeof(unsigned)), c->stream));
   return WRS_OK;
 }
 
@@ -198,10 +214,10 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
 
   if (t_kv == 0) {
     // attention.rs:93-96: zero output. Rows of out may be strided.
-    for (size_t b = 0; b < batch; ++b)
-      for (size_t h = 0; h < n_heads; ++h)
-        WRS_HIP(c, hipMemset2DAsync(out + b * lo.batch_stride + h * lo.head_stride,
-                                    lo.row_stride * 4, 0, d_head * 4, t_q, c->stream));
+    WRS_HIP(c, wrs::launch_fill_zero_rows(out, lo.batch_stride, lo.head_stride, lo.row_stride,
+                                          static_cast<int>(batch), static_cast<int>(n_heads),
+                                          static_cast<int>(t_q), static_cast<int>(d_head),
+                                          c->stream));
     return WRS_OK;
   }
 
@@ -226,6 +242,7 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
                 int n_heads) {
   const int n_groups = static_cast<int>(goff.size());
   if (n_groups == 0) return WRS_OK;
+  if (!kbase || !vbase) return fail(c, WRS_EINVAL, "decode over an unallocated K/V plane");
   if (n_groups > wrs::kMaxDecodeGroups || rows_per_group < 1 ||
       rows_per_group > wrs::kMaxRowsPerGroup)
     return fail(c, WRS_EINVAL, "decode batch shape");
@@ -291,6 +308,7 @@ const char* wrs_attn_status_string(int status) {
     case WRS_EHIP: return "HIP runtime error";
     case WRS_EUNSUPPORTED: return "unsupported on the GPU path";
     case WRS_ERANGE: return "index or length outside the arena";
+    case WRS_ECAPTURE: return "scratch would grow during graph capture (reserve it first)";
     default: return "unknown status";
   }
 }
@@ -330,7 +348,20 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
 int wrs_attn_set_stream(wrs_attn_ctx* c, void* s) {
   if (!c) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
-  c->stream = static_cast<hipStream_t>(s);
+  hipStream_t ns = static_cast<hipStream_t>(s);
+  if (ns != c->stream) {
+    // Work queued on the old stream may still use the context's scratch:
+    // drain it, unless either stream is recording a graph (a host wait is not
+    // allowed then, and the caller orders the streams).
+    DeviceGuard g(c->device);
+    hipStreamCaptureStatus so = hipStreamCaptureStatusNone, sn = hipStreamCaptureStatusNone;
+    const bool cap_old = hipStreamIsCapturing(c->stream, &so) == hipSuccess &&
+                         so != hipStreamCaptureStatusNone;
+    const bool cap_new =
+        hipStreamIsCapturing(ns, &sn) == hipSuccess && sn != hipStreamCaptureStatusNone;
+    if (!cap_old && !cap_new) WRS_HIP(c, hipStreamSynchronize(c->stream));
+  }
+  c->stream = ns;
   return WRS_OK;
 }
 
@@ -344,6 +375,65 @@ int wrs_attn_synchronize(wrs_attn_ctx* c) {
 }
 
 const char* wrs_attn_last_error(wrs_attn_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int wrs_stream_read(wrs_attn_ctx* c, const void* src, size_t bytes, float* sink,
+                    size_t sink_len) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (bytes == 0) return WRS_OK;
+  if (!src || !sink) return fail(c, WRS_EINVAL, "null argument");
+  if (bytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15))
+    return fail(c, WRS_EINVAL, "stream_read: 16-byte aligned multiple of 16 bytes");
+  if (sink_len < static_cast<size_t>(wrs::stream_read_blocks(static_cast<int64_t>(bytes))))
+    return fail(c, WRS_EINVAL, "stream_read: sink shorter than one float per workgroup");
+  DeviceGuard g(c->device);
+  WRS_HIP(c, wrs::launch_stream_read(src, static_cast<int64_t>(bytes), sink, c->stream));
+  return WRS_OK;
+}
+
+int wrs_attn_reserve(wrs_attn_ctx* c, const wrs_reserve* r) {
+  if (!c || !r) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard g(c->device);
+  if (!fits_int(r->n_heads) || !fits_int(r->decode_rows) || !fits_int(r->decode_keys) ||
+      !fits_int(r->capture_tokens) || !fits_int(r->capture_keys) ||
+      !fits_int(r->linear_tokens) || !fits_int(r->linear_n_in))
+    return fail(c, WRS_EINVAL, "wrs_attn_reserve: size exceeds 2^31");
+  int rc = WRS_OK;
+  const int heads = static_cast<int>(r->n_heads);
+  if (heads && r->decode_rows && r->decode_keys > static_cast<size_t>(wrs::kDecodeChunkLong)) {
+    // One decode launch: groups x rows_per_group query rows (a self step's
+    // slots, up to kMaxDecodeGroups, or an utterance's beams, up to
+    // kMaxRowsPerGroup), each row's partials per split of kDecodeChunk keys.
+    const int rows = static_cast<int>(std::min<size_t>(
+        r->decode_rows, std::max(wrs::kMaxDecodeGroups, wrs::kMaxRowsPerGroup)));
+    const int splits = static_cast<int>((r->decode_keys + wrs::kDecodeChunk - 1) / wrs::kDecodeChunk);
+    rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes,
+              wrs::decode_part_floats(rows, heads, splits, 1) * sizeof(float), false);
+    if (rc) return rc;
+    rc = grow(c, reinterpret_cast<void**>(&c->counters), &c->counter_bytes,
+              wrs::decode_counter_words(rows, heads) * sizeof(unsigned), true);
+    if (rc) return rc;
+  }
+  if (r->capture_tokens && r->capture_keys) {
+    rc = grow(c, reinterpret_cast<void**>(&c->cap_part), &c->cap_part_bytes,
+              wrs::capture_part_floats(wrs::kMaxCapturePairs, static_cast<int>(r->capture_tokens),
+                                       static_cast<int>(r->capture_keys)) * sizeof(float),
+              false);
+    if (rc) return rc;
+  }
+  if (r->linear_tokens > static_cast<size_t>(wrs::kGemvMaxRows) && r->linear_n_in) {
+    const size_t split_bytes =
+        align_up(r->linear_tokens * wrs::kSplitParts * r->linear_n_in * 2, 256);
+    rc = grow(c, &c->lin_x, &c->lin_x_bytes, split_bytes + r->linear_tokens * 4, false);
+    if (rc) return rc;
+    rc = grow(c, reinterpret_cast<void**>(&c->ln_x), &c->ln_x_bytes,
+              r->linear_tokens * r->linear_n_in * sizeof(float), false);
+    if (rc) return rc;
+  }
+  WRS_HIP(c, hipStreamSynchronize(c->stream));
+  return WRS_OK;
+}
 
 int wrs_single_token_mha_d64(wrs_attn_ctx* c, const float* q, size_t q_len, const float* k,
                              size_t k_len, const float* v, size_t v_len, size_t t_kv,
@@ -713,10 +803,11 @@ int wrs_kv_set_cross(wrs_kv* kv, size_t layer, const float* k, const float* v, s
   return WRS_OK;
 }
 
-int wrs_kv_cross_len(wrs_kv* kv, size_t* n_audio) {
+int wrs_kv_cross_len(wrs_kv* kv, size_t layer, size_t* n_audio) {
   if (!kv || !n_audio) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(kv->ctx->mu);
-  *n_audio = kv->cross_len.empty() ? 0 : kv->cross_len[0];
+  if (layer >= kv->n_layers) return fail(kv->ctx, WRS_ERANGE, "layer out of range");
+  *n_audio = kv->cross_len[layer];
   return WRS_OK;
 }
 
@@ -776,6 +867,12 @@ int wrs_attn_decode_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float
   DeviceGuard g(c->device);
   const int64_t dm = static_cast<int64_t>(kv->d_model());
   const size_t L = kv->cross_len[layer];
+  if (L == 0) {
+    // attention.rs:93-96: no keys, zero output (the plane may not exist).
+    WRS_HIP(c, wrs::launch_fill_zero_rows(out, 0, 0, dm, 1, 1, static_cast<int>(n_beams),
+                                          static_cast<int>(dm), c->stream));
+    return WRS_OK;
+  }
   // All beams of the utterance share one read of the plane; beyond 8 beams the
   // rows go in further launches of up to 8.
   for (size_t b0 = 0; b0 < n_beams; b0 += wrs::kMaxRowsPerGroup) {

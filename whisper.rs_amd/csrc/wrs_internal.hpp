@@ -100,6 +100,12 @@ hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s);
 size_t decode_part_floats(int n_groups, int n_heads, int n_splits, int rows);
 size_t decode_counter_words(int n_groups, int n_heads);
 
+// Measurement: a streaming read of `bytes` (multiple of 16, 16-byte aligned)
+// with the split-K decode's grid shape (512 threads x 64 bytes per
+// workgroup); sink receives stream_read_blocks(bytes) floats.
+hipError_t launch_stream_read(const void* src, int64_t bytes, float* sink, hipStream_t s);
+int64_t stream_read_blocks(int64_t bytes);
+
 // Alignment-head capture over the f16 cross plane
 // (decoder.rs:796-828 semantics): for query row i and pair p,
 // softmax_j(dot(q_i[head_p], k_j[head_p]) * scale) into
@@ -172,6 +178,13 @@ hipError_t launch_layer_norm(const float* x, const float* gamma, const float* be
                              int n_tokens, int d, DType out_dt, void* out, hipStream_t s);
 // GELU, tanh form, in place on f32 (gelu.rs:11-23); data 16-byte aligned.
 hipError_t launch_gelu(float* data, int64_t n, hipStream_t s);
+
+// Zero fills issued as kernels (never as memset nodes, so that a caller may
+// capture them into a graph): f32 element (b, h, r, c) at
+// base + b*bs + h*hs + r*rs + c for c < cols; and n 32-bit words.
+hipError_t launch_fill_zero_rows(float* base, int64_t bs, int64_t hs, int64_t rs, int batch,
+                                 int n_heads, int n_rows, int cols, hipStream_t s);
+hipError_t launch_fill_zero_u32(unsigned* p, int64_t n, hipStream_t s);
 
 // KV arena kernels.
 // f32 rows [n][d_model] (row stride src_rs) -> f16 planes: head h, row i at
