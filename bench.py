@@ -447,13 +447,13 @@ def bench_weight_stream(wrs, W, ctx, reps, eager=False):
             else:
                 wrs.linear(x, w, None, o, ctx=ctx)
 
-    step()
-    torch.cuda.synchronize()
-    if eager:
+    if eager:  # exactly `reps` steps, nothing else (counter passes)
         for _ in range(reps):
             step()
         torch.cuda.synchronize()
         return cfg, len(calls)
+    step()
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         ctx.use_torch_stream()
@@ -658,8 +658,8 @@ def calibration_copy():
 
 # kernel-name patterns of each leg in the counter passes (demangled names)
 TRAFFIC_LEGS = {
-    "encoder": (r"fa2_prefill_d64<__bf16>", None),
-    "encoder_base": (r"fa2_prefill_d64<_Float16>", None),
+    "encoder": (r"fa2_prefill_d64<(__bf16|bf16|std::bfloat16_t|DF16b)", None),
+    "encoder_base": (r"fa2_prefill_d64<(_Float16|half|DF16_)", None),
     "decode": (r"decode_f16<\s*5\s*,", None),
     "decode_self": (r"decode_f16<\s*1\s*,", None),
     "capture": (r"capture_cross", None),
@@ -708,6 +708,9 @@ def measure_traffic(extra: list[str]):
                 log(f"traffic: {counter}: no calibration copy in the profile")
                 return None
             factor = CALIB_BYTES / (max(copy) * 1024.0)
+            if counter == "FETCH_SIZE":
+                log("traffic: kernels profiled: " +
+                    "; ".join(f"{n[:90]} x{c}" for n, _, _, _, c in rows))
             for leg, (pat, mode) in TRAFFIC_LEGS.items():
                 hit = [(n, av, tot, cnt) for n, av, _, tot, cnt in rows if re.search(pat, n)]
                 if not hit:
