@@ -197,6 +197,18 @@ int wrs_attn_decode_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const size
  * n_audio_max = 0) gives zero rows, as t_kv == 0 does (attention.rs:93-96). */
 int wrs_attn_decode_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
                           size_t n_beams, float *out);
+/* Allocation-free variant of wrs_attn_decode_cross, with the same arguments
+ * and results. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Its split-K partials and merge counters
+ * live in a fixed device array of the library (2 MiB + 64 KiB, one per GPU,
+ * held until the process ends), so it never calls hipMalloc or hipFree; a
+ * shape whose partials do not fit (beams x heads x ceil(n_audio / 128) x 68
+ * floats above 524288, or more than 16384 heads) fails with WRS_ERANGE. Every
+ * call on one GPU shares that array: calls that overlap on one GPU (other
+ * streams, other contexts) race. */
+int wrs_attn_decode_cross_noalloc(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
+                                  size_t n_beams, float *out);
 /* Multi-token rows (prompt prefill): decoder.rs:857-891 self-attention with
  * offset t_past = slot_len(slot) over the slot's f16 cache (rows appended),
  * and attention.rs:107-243 cross-attention with t_q = n_tokens. */

@@ -144,6 +144,10 @@ pub mod ffi {
             slots: *const usize, n: usize, q: *const f32, out: *mut f32) -> c_int;
         pub fn wrs_attn_decode_cross(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
             q: *const f32, n_beams: usize, out: *mut f32) -> c_int;
+        // allocation-free decode_cross (no reference counterpart): fixed scratch,
+        // for callers that cannot allocate (graph capture, serving loops)
+        pub fn wrs_attn_decode_cross_noalloc(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
+            q: *const f32, n_beams: usize, out: *mut f32) -> c_int;
         pub fn wrs_attn_prefill_self(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
             slot: usize, q: *const f32, n_tokens: usize, out: *mut f32) -> c_int;
         pub fn wrs_attn_prefill_cross(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
@@ -369,6 +373,16 @@ impl<'c> KvArena<'c> {
     pub unsafe fn decode_cross(&self, layer: usize, q: *const f32, n_beams: usize,
                                out: *mut f32) {
         self.ctx.check(wrs_attn_decode_cross(self.ctx.raw(), self.kv, layer, q, n_beams, out));
+    }
+    /// `decode_cross` on the library's fixed device scratch: allocates nothing
+    /// (usable under graph capture); calls on one GPU must not overlap.
+    ///
+    /// # Safety
+    /// As for [`KvArena::decode_cross`].
+    pub unsafe fn decode_cross_noalloc(&self, layer: usize, q: *const f32, n_beams: usize,
+                                       out: *mut f32) {
+        self.ctx.check(wrs_attn_decode_cross_noalloc(self.ctx.raw(), self.kv, layer, q,
+                                                     n_beams, out));
     }
 }
 

@@ -424,6 +424,13 @@ class KvArena:
                                                 q.data_ptr(), n, out.data_ptr()),
                 "decode_cross")
 
+    def decode_cross_noalloc(self, layer, q, out, n_beams=None):
+        """decode_cross on the library's fixed device scratch: allocates nothing."""
+        n = q.shape[0] if n_beams is None else n_beams
+        self._c(self._lib.wrs_attn_decode_cross_noalloc(self.ctx.handle, self.handle, layer,
+                                                        q.data_ptr(), n, out.data_ptr()),
+                "decode_cross_noalloc")
+
     def prefill_self(self, layer, slot, q, out):
         self._c(self._lib.wrs_attn_prefill_self(self.ctx.handle, self.handle, layer, slot,
                                                 q.data_ptr(), q.shape[0], out.data_ptr()),

@@ -85,6 +85,7 @@ _SIGNATURES = {
     "wrs_kv_cross_planes": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
     "wrs_attn_decode_self": (_int, [_vp, _vp, _sz, _szp, _sz, _vp, _vp]),
     "wrs_attn_decode_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "wrs_attn_decode_cross_noalloc": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_self": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "wrs_linear": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _vp, _vp, _sz, _sz, _sz, _int,

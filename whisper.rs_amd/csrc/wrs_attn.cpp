@@ -17,6 +17,14 @@
 
 using wrs::DType;
 
+// Fixed scratch of the allocation-free cross decode
+// (wrs_attn_decode_cross_noalloc): f32 split-K partials, then the merge
+// counters. Each GPU the library runs on holds its own copy until the process
+// ends; every call on that GPU shares it, so such calls must not overlap.
+constexpr size_t kNoallocPartBytes = size_t{2} << 20;       // 524288 f32 partials
+constexpr size_t kNoallocCounterBytes = size_t{64} << 10;   // 16384 counter words
+static __device__ __align__(256) unsigned char scratch[kNoallocPartBytes + kNoallocCounterBytes];
+
 struct wrs_attn_ctx {
   int device = 0;
   hipStream_t own_stream = nullptr;
@@ -236,10 +244,51 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
   return WRS_OK;
 }
 
+// Device addresses of `scratch`, one per GPU: the array's host-side name is
+// not a device address, so kernels and fills only ever see these.
+constexpr int kMaxNoallocDevices = 64;
+struct NoallocScratch {
+  std::mutex mu;
+  unsigned char* ptr[kMaxNoallocDevices] = {};
+};
+NoallocScratch& noalloc_scratch() {
+  static NoallocScratch s;
+  return s;
+}
+
+// Once per device, with that device current (the caller holds a DeviceGuard):
+// resolve the array's address on this GPU and clear its merge counters.
+int noalloc_setup(wrs_attn_ctx* c) {
+  if (c->device >= kMaxNoallocDevices) return WRS_OK;  // the entry point refuses later
+  NoallocScratch& ns = noalloc_scratch();
+  std::lock_guard<std::mutex> lk(ns.mu);
+  if (ns.ptr[c->device]) return WRS_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) return fail(c, WRS_EHIP, "hipGetSymbolAddress(scratch)", e);
+  unsigned char* base = static_cast<unsigned char*>(p);
+  WRS_HIP(c, wrs::launch_fill_zero_u32(reinterpret_cast<unsigned*>(base + kNoallocPartBytes),
+                                       static_cast<int64_t>(kNoallocCounterBytes / 4),
+                                       c->stream));
+  WRS_HIP(c, hipStreamSynchronize(c->stream));
+  ns.ptr[c->device] = base;
+  return WRS_OK;
+}
+
+unsigned char* noalloc_ptr(int device) {
+  if (device < 0 || device >= kMaxNoallocDevices) return nullptr;
+  NoallocScratch& ns = noalloc_scratch();
+  std::lock_guard<std::mutex> lk(ns.mu);
+  return ns.ptr[device];
+}
+
+// Split-K decode over f16 planes. `fixed` (the device address of `scratch`)
+// replaces the context's scratch and is never grown: shapes whose partials or
+// counters do not fit fail with WRS_ERANGE.
 int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64_t o_rs,
                 const uint16_t* kbase, const uint16_t* vbase, int64_t kv_hs,
                 const std::vector<int64_t>& goff, const std::vector<int>& lens, int rows_per_group,
-                int n_heads) {
+                int n_heads, unsigned char* fixed = nullptr) {
   const int n_groups = static_cast<int>(goff.size());
   if (n_groups == 0) return WRS_OK;
   if (!kbase || !vbase) return fail(c, WRS_EINVAL, "decode over an unallocated K/V plane");
@@ -273,14 +322,26 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
   if (a.n_splits > 1) {
     const size_t pb =
         wrs::decode_part_floats(n_groups, n_heads, a.n_splits, rows_per_group) * sizeof(float);
-    int rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes, pb, false);
-    if (rc) return rc;
-    rc = grow(c, reinterpret_cast<void**>(&c->counters), &c->counter_bytes,
-              wrs::decode_counter_words(n_groups, n_heads) * sizeof(unsigned), true);
-    if (rc) return rc;
+    const size_t cb = wrs::decode_counter_words(n_groups, n_heads) * sizeof(unsigned);
+    if (fixed) {
+      if (pb > kNoallocPartBytes || cb > kNoallocCounterBytes)
+        return fail(c, WRS_ERANGE,
+                    "decode shape needs more than the fixed scratch (2 MiB of partials, "
+                    "64 KiB of counters)");
+    } else {
+      int rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes, pb, false);
+      if (rc) return rc;
+      rc = grow(c, reinterpret_cast<void**>(&c->counters), &c->counter_bytes, cb, true);
+      if (rc) return rc;
+    }
   }
-  a.part = c->part;
-  a.counters = c->counters;
+  if (fixed) {
+    a.part = reinterpret_cast<float*>(fixed);
+    a.counters = reinterpret_cast<unsigned*>(fixed + kNoallocPartBytes);
+  } else {
+    a.part = c->part;
+    a.counters = c->counters;
+  }
   WRS_HIP(c, wrs::launch_decode_f16(a, c->stream));
   return WRS_OK;
 }
@@ -327,6 +388,12 @@ int wrs_attn_create(int device, wrs_attn_ctx** out) {
     return WRS_EHIP;
   }
   c->stream = c->own_stream;
+  const int rc = noalloc_setup(c);
+  if (rc) {
+    (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return rc;
+  }
   *out = c;
   return WRS_OK;
 }
@@ -857,10 +924,12 @@ int wrs_attn_decode_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const size_t
   return WRS_OK;
 }
 
-int wrs_attn_decode_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
-                          size_t n_beams, float* out) {
-  if (!c || !kv) return WRS_EINVAL;
-  std::lock_guard<std::mutex> lk(c->mu);
+}  // extern "C"
+
+namespace {
+
+int decode_cross_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                      size_t n_beams, float* out, unsigned char* fixed) {
   if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
   if (n_beams == 0) return WRS_OK;
   if (!q || !out) return fail(c, WRS_EINVAL, "null argument");
@@ -874,17 +943,38 @@ int wrs_attn_decode_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float
     return WRS_OK;
   }
   // All beams of the utterance share one read of the plane; beyond 8 beams the
-  // rows go in further launches of up to 8.
+  // rows go in further launches of up to 8 (which reuse the same scratch in
+  // stream order).
   for (size_t b0 = 0; b0 < n_beams; b0 += wrs::kMaxRowsPerGroup) {
     const size_t rows = std::min<size_t>(wrs::kMaxRowsPerGroup, n_beams - b0);
     std::vector<int64_t> goff(1, static_cast<int64_t>(kv->cross_off(layer)));
     std::vector<int> lens(1, static_cast<int>(L));
     int rc = decode_impl(c, q + b0 * dm, dm, out + b0 * dm, dm, kv->k_cross, kv->v_cross,
                          static_cast<int64_t>(kv->n_audio_max * 64), goff, lens,
-                         static_cast<int>(rows), static_cast<int>(kv->n_heads));
+                         static_cast<int>(rows), static_cast<int>(kv->n_heads), fixed);
     if (rc) return rc;
   }
   return WRS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wrs_attn_decode_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                          size_t n_beams, float* out) {
+  if (!c || !kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  return decode_cross_impl(c, kv, layer, q, n_beams, out, nullptr);
+}
+
+int wrs_attn_decode_cross_noalloc(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                                  size_t n_beams, float* out) {
+  if (!c || !kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  unsigned char* fixed = noalloc_ptr(c->device);
+  if (!fixed) return fail(c, WRS_EUNSUPPORTED, "no fixed scratch on this device");
+  return decode_cross_impl(c, kv, layer, q, n_beams, out, fixed);
 }
 
 int wrs_attn_prefill_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, size_t slot, const float* q,
