@@ -658,8 +658,9 @@ def calibration_copy():
 
 # kernel-name patterns of each leg in the counter passes (demangled names)
 TRAFFIC_LEGS = {
-    "encoder": (r"fa2_prefill_d64<(__bf16|bf16|std::bfloat16_t|DF16b)", None),
-    "encoder_base": (r"fa2_prefill_d64<(_Float16|half|DF16_)", None),
+    # demangled (fa2_prefill_d64<__bf16>) or mangled (fa2_prefill_d64IDF16b...)
+    "encoder": (r"fa2_prefill_d64(?:<\s*|I)(?:__bf16|bf16|DF16b)", None),
+    "encoder_base": (r"fa2_prefill_d64(?:<\s*|I)(?:_Float16|half|DF16_)", None),
     "decode": (r"decode_f16<\s*5\s*,", None),
     "decode_self": (r"decode_f16<\s*1\s*,", None),
     "capture": (r"capture_cross", None),

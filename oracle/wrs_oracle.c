@@ -481,7 +481,7 @@ int wrs_oracle_materialized_attention(const float *q, const float *k, const floa
 #endif
     for (size_t h = 0; h < n_heads; ++h) {
         const size_t ho = h * d_head;
-        float *scores = (float *)malloc(sizeof(float) * (t_q * t_kv ? t_q * t_kv : 1));
+        float *scores = (float *)malloc(sizeof(float) * (t_q > 0 && t_kv > 0 ? t_q * t_kv : 1));
         if (!scores) {
 #ifdef _OPENMP
 #pragma omp atomic write

@@ -149,10 +149,14 @@ def test_large_encoder_bf16(wrs, orc, ctx):
     q, k, v = cfg.inputs()
     out = _encoder_run(wrs, ctx, cfg, q, k, v, torch.bfloat16)
     assert np.all(np.isfinite(out))
-    # oracle on the first and last window, all 20 heads
-    for w in (0, cfg.batch - 1):
+    # every window, all 20 heads, against the oracle; the worst error of each
+    # window is printed (pytest -s) before the bound is checked
+    worst = []
+    for w in range(cfg.batch):
         ref = _oracle_fa2(orc, q[w], k[w], v[w], cfg.t, cfg.t, cfg.n_heads, cfg.d_model)
-        assert maxerr(out[w], ref) <= TOL16, f"window {w}"
+        worst.append(maxerr(out[w], ref))
+        note(f"  window {w:2d}: max|gpu - oracle| = {worst[-1]:.3e}")
+    assert max(worst) <= TOL16, [f"{e:.3e}" for e in worst]
     # every window: each output is a convex combination of that head's V rows
     vmin = v.min(axis=1)
     vmax = v.max(axis=1)
@@ -369,3 +373,125 @@ def test_prefill_rescale_paths(wrs, ctx, profile):
     assert np.all(np.isfinite(got))
     ref = attention_f64(q, k, v, t_q, t_kv, H, dm)
     assert maxerr(got, ref) <= TOL16
+
+
+# ---- the reference benchmark's largest shape ------------------------------------
+
+def _bench_inputs(orc, t_q, t_kv, d_model):
+    # crates/tensor/tests/bench_flash_attention_tiled.rs:142-146: one xorshift
+    # stream, q then k then v, uniform in [-1, 1]
+    rng = orc.Rng(0x5EED1234)
+    return rng.fill(t_q * d_model), rng.fill(t_kv * d_model), rng.fill(t_kv * d_model)
+
+
+def test_host_slice_bench_shape_4096(wrs, orc, ctx):
+    # (4096, 4096), 6 heads of 64 (bench_flash_attention_tiled.rs:19-25) through
+    # the f32 drop-in: the oracle's tiled and materialized results at 1e-5
+    t, H, dm = 4096, 6, 384
+    note("host-slice flash_attention_2 t_q=t_kv=4096, 6 heads, f32")
+    q, k, v = _bench_inputs(orc, t, t, dm)
+    out = np.full(t * dm, np.nan, np.float32)
+    wrs.flash_attention_2(q, k, v, t, t, H, dm, False, out, ctx=ctx)
+    tiled = np.zeros(t * dm, np.float32)
+    orc.flash_attention_2(q, k, v, t, t, H, dm, False, tiled)
+    mat = np.zeros(t * dm, np.float32)
+    orc.materialized_attention(q, k, v, t, t, H, dm, mat)
+    e_t, e_m = maxerr(out, tiled), maxerr(out, mat)
+    note(f"  max|gpu - tiled| = {e_t:.3e}, max|gpu - materialized| = {e_m:.3e}")
+    assert e_t <= TOL32 and e_m <= TOL32
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_device_prefill_bench_shape_4096(wrs, orc, ctx, dtype):
+    # the same shape on the 16-bit MFMA kernel, inputs rounded to the storage
+    # type and widened exactly for the oracle
+    from wrs_amd import workloads as W
+    t, H, dm = 4096, 6, 384
+    note(f"device prefill {dtype} t_q=t_kv=4096, 6 heads")
+    q, k, v = (W._round(x.reshape(t, dm), dtype) for x in _bench_inputs(orc, t, t, dm))
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    out = torch.full((t, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lay = wrs.token_major(t, dm, 64)
+    wrs.prefill(dev(q, tdt), dev(k, tdt), dev(v, tdt), out, batch=1, n_heads=H, t_q=t, t_kv=t,
+                d_head=64, q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+    ref = _oracle_fa2(orc, q, k, v, t, t, H, dm)
+    e = maxerr(host(out), ref)
+    note(f"  max|gpu - oracle| = {e:.3e}")
+    assert e <= TOL16
+
+
+# ---- bf16 V outside the f16 range: listed blocks recomputed in f32 ---------------
+
+def _colscaled_err(got, ref, v):
+    # output column d is a convex combination of V[:, d]: its f32 rounding error
+    # scales with max_k |V[k, d]|
+    scale = np.maximum(1.0, np.abs(v).max(axis=0))
+    return float((np.abs(got - ref) / scale).max())
+
+
+def _bf16_run(wrs, ctx, q, k, v, B, H, T):
+    dm = H * 64
+    lay = wrs.token_major(T, dm, 64)
+    out = torch.full((B, T, dm), float("nan"), dtype=torch.float32, device="cuda")
+    wrs.prefill(dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(v, torch.bfloat16), out,
+                batch=B, n_heads=H, t_q=T, t_kv=T, d_head=64, q_layout=lay, kv_layout=lay,
+                out_layout=lay, ctx=ctx)
+    return host(out)
+
+
+def test_bf16_v_beyond_f16_range(wrs, orc, ctx):
+    # The 16-bit kernel widens bf16 V to f16 in LDS; |v| >= 65536 has no f16
+    # value. Those blocks come out non-finite, are listed, and are recomputed by
+    # the f32 kernel from the bf16 inputs, so the result is finite and matches
+    # the oracle (the reference works in f32: attention.rs:68-243). Other
+    # (batch, head) pairs keep the 16-bit kernel's bits, and the list is empty
+    # again afterwards: a clean call repeats its first result bitwise.
+    from wrs_amd import workloads as W
+    B, H, T = 2, 3, 600
+    dm = H * 64
+    note("device prefill bf16 with V values of magnitude 1e5 in one head")
+    q = W.normal((B, T, dm), 71, storage="bf16")
+    k = W.normal((B, T, dm), 72, storage="bf16")
+    v = W.normal((B, T, dm), 73, storage="bf16")
+    clean = _bf16_run(wrs, ctx, q, k, v, B, H, T)
+    big = v.copy()
+    big[1, 123, 2 * 64 + 5] = 1.0e5       # batch 1, head 2
+    big[1, 400, 2 * 64 + 60] = -3.0e38    # near the bf16 maximum
+    big = W._round(big, "bf16")
+    got = _bf16_run(wrs, ctx, q, k, big, B, H, T)
+    assert np.all(np.isfinite(got))
+    for b in range(B):
+        ref = _oracle_fa2(orc, q[b], k[b], big[b], T, T, H, dm)
+        for h in range(H):
+            sl = slice(h * 64, (h + 1) * 64)
+            err = maxerr(got[b][:, sl], ref[:, sl])
+            rel = _colscaled_err(got[b][:, sl], ref[:, sl], big[b, :, sl])
+            note(f"  batch {b} head {h}: max|gpu - oracle| = {err:.3e}, "
+                 f"over max|V column| {rel:.3e}")
+            if (b, h) == (1, 2):
+                assert rel <= TOL32
+            else:
+                assert err <= TOL16
+                assert np.array_equal(got[b][:, sl], clean[b][:, sl]), (b, h)
+    again = _bf16_run(wrs, ctx, q, k, v, B, H, T)
+    assert np.array_equal(again, clean)
+
+
+def test_bf16_v_beyond_f16_range_everywhere(wrs, orc, ctx):
+    # Every block of the large-v3 encoder batch (16 windows x 20 heads) meets an
+    # out-of-range V value: more listed blocks than the list holds, so every
+    # block is recomputed in f32. Windows 0 and 15 against the oracle.
+    from wrs_amd import workloads as W
+    cfg = W.LARGE_ENCODER
+    note("device prefill bf16 large-v3 batch, V = 7e4 at key 700 of every head")
+    q, k, v = cfg.inputs()
+    v = v.copy()
+    v[:, 700, ::64] = 7.0e4
+    v = W._round(v, "bf16")
+    out = _encoder_run(wrs, ctx, cfg, q, k, v, torch.bfloat16)
+    assert np.all(np.isfinite(out))
+    for w in (0, cfg.batch - 1):
+        ref = _oracle_fa2(orc, q[w], k[w], v[w], cfg.t, cfg.t, cfg.n_heads, cfg.d_model)
+        rel = _colscaled_err(out[w], ref, v[w])
+        note(f"  window {w}: max|gpu - oracle| over max|V column| = {rel:.3e}")
+        assert rel <= TOL32

@@ -89,6 +89,34 @@ __device__ inline float ld_agent(const float* p) {
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
 __device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
 
+// x op x[lane ^ 32] and x op x[lane ^ 16] with the gfx950 lane-swap VALU
+// instructions (no LDS round trip). Issued as inline asm on two distinct
+// registers: the swap writes both operands.
+__device__ inline void swap32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ inline void swap16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ inline float max_x16_x32(float x) {
+  float a = x, b = x;
+  swap16(a, b);  // a, b: x of this row and of the row 16 lanes away
+  x = fmaxf(a, b);
+  a = x;
+  b = x;
+  swap32(a, b);
+  return fmaxf(a, b);
+}
+__device__ inline float sum_x16_x32(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  x = a + b;
+  a = x;
+  b = x;
+  swap32(a, b);
+  return a + b;
+}
+
 
 // kMWaves waves of one 16-key tile each: 8 (128 keys, kDecodeChunk) in
 // general, 16 (kDecodeChunkLong = 256 keys) when that covers the whole
@@ -108,16 +136,16 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   const int col = lane & 15, kg = lane >> 4;
   const bool lo_part = col >= 8;
 
-  const int qrow = col & 7;
-  float qv[16];
-  {
-    const float* qp = a.q + static_cast<int64_t>(g * rows + (qrow < rows ? qrow : 0)) * a.q_rs + h * 64 + 8 * kg;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      qv[j] = qp[j];
-      qv[8 + j] = qp[32 + j];
-    }
-  }
+  // q rows of the group, staged once per workgroup: thread t < rows*16 loads
+  // 4 values (row t/16), scales them by scale*log2(e) and by the power of two
+  // that puts the row's largest magnitude into [2^14, 2^15), and stores them.
+  __shared__ __attribute__((aligned(16))) float qs[8][64];
+  __shared__ float qdown[8];
+  const bool qload = tid < rows * 16;
+  f32x4 qx = {0.f, 0.f, 0.f, 0.f};
+  if (qload)
+    qx = *reinterpret_cast<const f32x4*>(a.q + static_cast<int64_t>(g * rows + (tid >> 4)) * a.q_rs +
+                                         h * 64 + 4 * (tid & 15));
   // Lane (col, kg) carries key kbase + col: d 8kg..8kg+7 and 32+8kg.. of its
   // K and V rows (the A-operand layout of a 16x16x32 MFMA).
   const int kbase = split * kChunk + wave * 16;
@@ -137,24 +165,43 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   // arithmetic below depends on a value defined after them.
   float one;
   __asm__ volatile("v_mov_b32 %0, 1.0" : "=v"(one) : : "memory");
-
-  // q * scale * log2(e), scaled by 2^sh so the row max lies in [2^14, 2^15),
-  // split into f16 high (columns 0-7 of B) and low (columns 8-15) parts.
-  float amax = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    qv[j] = (qrow < rows ? qv[j] : 0.f) * (a.scale_log2 * one);
-    amax = fmaxf(amax, fabsf(qv[j]));
+  if (qload) {
+    qx *= a.scale_log2 * one;
+    float amax = fmaxf(fmaxf(fabsf(qx[0]), fabsf(qx[1])), fmaxf(fabsf(qx[2]), fabsf(qx[3])));
+    amax = fmaxf(amax, dpp<0xB1>(amax));   // the row's 16 lanes (DPP inside a row)
+    amax = fmaxf(amax, dpp<0x4E>(amax));
+    amax = fmaxf(amax, dpp<0x141>(amax));
+    amax = fmaxf(amax, dpp<0x140>(amax));
+    const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+    const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
+    *reinterpret_cast<f32x4*>(&qs[tid >> 4][4 * (tid & 15)]) = qx * pow2(sh);
+    if ((tid & 15) == 0) qdown[tid >> 4] = pow2(clamp_exp(-sh));
   }
-  amax = fmaxf(amax, __shfl_xor(amax, 16));
-  amax = fmaxf(amax, __shfl_xor(amax, 32));
-  const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
-  const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
-  const float up = pow2(sh), down = pow2(clamp_exp(-sh));
+  __syncthreads();
+
+  // Split into f16 high (columns 0-7 of B) and low (columns 8-15) parts; rows
+  // past the group's are zero.
+  const int qrow = col & 7;
+  const float down = qrow < rows ? qdown[qrow] : 1.f;
+  float qv[16];
+  {
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 q0 = qrow < rows ? *reinterpret_cast<const f32x4*>(&qs[qrow][8 * kg]) : z4;
+    const f32x4 q1 = qrow < rows ? *reinterpret_cast<const f32x4*>(&qs[qrow][8 * kg + 4]) : z4;
+    const f32x4 q2 = qrow < rows ? *reinterpret_cast<const f32x4*>(&qs[qrow][32 + 8 * kg]) : z4;
+    const f32x4 q3 = qrow < rows ? *reinterpret_cast<const f32x4*>(&qs[qrow][36 + 8 * kg]) : z4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qv[j] = q0[j];
+      qv[4 + j] = q1[j];
+      qv[8 + j] = q2[j];
+      qv[12 + j] = q3[j];
+    }
+  }
   f16x8 b0, b1;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float x0 = qv[j] * up, x1 = qv[8 + j] * up;
+    const float x0 = qv[j], x1 = qv[8 + j];
     const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
     b0[j] = lo_part ? static_cast<_Float16>(x0 - static_cast<float>(h0)) : h0;
     b1[j] = lo_part ? static_cast<_Float16>(x1 - static_cast<float>(h1)) : h1;
@@ -173,8 +220,7 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
     sc[i] = (kbase + 4 * kg + i < len) ? full : -INFINITY;
     mx = fmaxf(mx, sc[i]);
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = max_x16_x32(mx);
   float sum = 0.f;
   f16x4 pa;
 #pragma unroll
@@ -184,8 +230,7 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
     const _Float16 ph = static_cast<_Float16>(p);
     pa[i] = lo_part ? static_cast<_Float16>(p - static_cast<float>(ph)) : ph;
   }
-  sum += __shfl_xor(sum, 16);
-  sum += __shfl_xor(sum, 32);
+  sum = sum_x16_x32(sum);
 
   // V^T by multiplying with a 0/1 selection matrix (exact), then P V.
   f16x8 e0, e1;

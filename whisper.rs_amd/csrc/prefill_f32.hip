@@ -1,34 +1,17 @@
 // K4: flash-attention prefill with f32 operands on gfx950 f32 MFMA
 // (v_mfma_f32_32x32x2_f32), for the 1e-5 accumulate-check runs and for the
 // shapes the 16-bit kernel does not take (d_head != 64, f32 queries against
-// the f16 decoder cache).
-//
-// Semantics are those of crates/tensor/src/ops/attention.rs:68-243, step by
-// step: s = scale * (q.k) (:141-156, alpha applied after the dot product),
-// per-tile m_new = max(m, max_j s_j), alpha = 0 if m == -inf else
-// exp(m - m_new) (:179-183), p = exp(s - m_new), l = l*alpha + sum p,
-// acc = acc*alpha + P V, out = acc * (1/l) or 0 (:228-241). Only the
-// summation order of the two products differs (MFMA instead of sgemm). K/V
-// given as f16/bf16 are widened exactly to f32.
-//
-// Decomposition: 4 waves x 32 queries per workgroup, 32-key tiles; like K1 the
-// wave computes S^T = K Q^T so each lane owns one query and its softmax
-// statistics.
-#include "wrs_internal.hpp"
+// the f16 decoder cache). One workgroup runs one 128-query block
+// (prefill_f32_block.hpp holds the block routine and its semantics).
+#include "prefill_f32_block.hpp"
 
 namespace wrs {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kM = 128;
-constexpr int kN = 32;
-constexpr int kThreads = 256;
-
-template <typename T>
-__device__ inline float widen(T x) {
-  return static_cast<float>(x);
-}
+using f32blk::fa2_block;
+using f32blk::kM;
+using f32blk::kThreads;
+using f32blk::Tiles;
 
 __device__ inline int xcd_remap(int pid, int nwg) {
   const int xcd = pid & 7, k = pid >> 3;
@@ -36,117 +19,12 @@ __device__ inline int xcd_remap(int pid, int nwg) {
   return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
 }
 
-// DB: number of 32-wide blocks covering d_head (d_head <= 32*DB).
 template <typename QT, typename KT, int DB>
 __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, int n_qblk) {
-  constexpr int D = 32 * DB;
-  constexpr int P = D + 1;  // odd LDS pitch: the 32 rows of one read hit distinct banks
-  __shared__ float Ks[kN * P];
-  __shared__ float Vs[kN * P];
-
+  __shared__ Tiles<DB> tl;
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int qblk = lid % n_qblk;
   const int bh = lid / n_qblk;
-  const int h = bh % a.n_heads;
-  const int b = bh / a.n_heads;
-  const int dh = a.d_head;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int r32 = lane & 31, hl = lane >> 5;
-
-  const QT* qp = static_cast<const QT*>(a.q) + b * a.lq.bs + h * a.lq.hs;
-  const KT* kp = static_cast<const KT*>(a.k) + b * a.lk.bs + h * a.lk.hs;
-  const KT* vp = static_cast<const KT*>(a.v) + b * a.lv.bs + h * a.lv.hs;
-
-  const int qi = qblk * kM + wave * 32 + r32;
-  const int qpos = qi + a.q_pos_offset;
-  // B operand of step kk: Q[qi][2*kk + hl].
-  float qf[D / 2];
-#pragma unroll
-  for (int kk = 0; kk < D / 2; ++kk) {
-    const int d = 2 * kk + hl;
-    qf[kk] = (qi < a.t_q && d < dh) ? widen(qp[static_cast<int64_t>(qi) * a.lq.rs + d]) : 0.f;
-  }
-
-  int kv_end = a.t_kv;
-  if (a.causal) {
-    const int last = min(qblk * kM + kM, a.t_q) - 1 + a.q_pos_offset;
-    kv_end = min(kv_end, last + 1);
-  }
-
-  f32x16 o[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) o[db] = f32x16{};
-  float m = -INFINITY, l = 0.f;
-
-  for (int j0 = 0; j0 < kv_end; j0 += kN) {
-    __syncthreads();
-    for (int e = tid; e < kN * D; e += kThreads) {
-      const int key = e / D, d = e % D;
-      float kv = 0.f, vv = 0.f;
-      if (j0 + key < a.t_kv && d < dh) {
-        kv = widen(kp[static_cast<int64_t>(j0 + key) * a.lk.rs + d]);
-        vv = widen(vp[static_cast<int64_t>(j0 + key) * a.lv.rs + d]);
-      }
-      Ks[key * P + d] = kv;
-      Vs[key * P + d] = vv;
-    }
-    __syncthreads();
-
-    f32x16 s = {};
-#pragma unroll
-    for (int kk = 0; kk < D / 2; ++kk)
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk], s, 0, 0, 0);
-
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = j0 + 8 * (i >> 2) + 4 * hl + (i & 3);
-      float x = a.scale * s[i];
-      if (key >= a.t_kv || (a.causal && key > qpos)) x = -INFINITY;
-      s[i] = x;
-      mx = fmaxf(mx, x);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    m = m_new;
-    float ls = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[i] = expf(s[i] - m_use);
-      ls += s[i];
-    }
-    l = l * alpha + ls;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) o[db] *= alpha;
-
-    // O^T += V^T P^T; step t contracts tile key 8*(t/4) + 4*hl + t%4, which is
-    // the key this lane's accumulator register t holds.
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int key = 8 * (t >> 2) + 4 * hl + (t & 3);
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * P + db * 32 + r32], s[t], o[db],
-                                                     0, 0, 0);
-    }
-  }
-
-  l += __shfl_xor(l, 32);
-  const float inv = (l > 0.f) ? 1.f / l : 0.f;
-  if (qi < a.t_q) {
-    float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(qi) * a.lo.rs;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (d < dh) op[d] = o[db][i] * inv;
-      }
-  }
+  fa2_block<QT, KT, DB>(a, lid % n_qblk, bh % a.n_heads, bh / a.n_heads, tl);
 }
 
 template <typename QT, typename KT>

@@ -34,11 +34,19 @@
 // land (exact in the f16 normal range).
 //
 // Softmax rescaling is lazy: weights are formed against a reference max that
-// may lag the true row max; a rescale (move the reference to the row max,
-// scale O and l, form the weights again) happens only when some query's row
-// sum over a step exceeds 2^14, which also bounds every weight inside the f16
-// range. The first step takes its reference max from its own (masked) scores
-// before forming its weights, so it never forms them twice.
+// may lag the true row max. A step is checked when some query's row sum over
+// it exceeds 2^14 (which bounds every weight inside the f16 range) or twice
+// the query's row sum over all earlier steps. Then every query whose step max
+// lies above its reference moves the reference there (scaling O and l), and,
+// if any did, the step's weights are formed again. The second condition puts
+// the reference on the dominant key of a peaked row, whose weight is then
+// exactly 1 instead of an f16-rounded value up to 2^14: with rounded dominant
+// weights the error reaches 2^-12 of the V range, with exact ones it stays
+// near the diffuse rows' level. A diffuse row rarely has one step outweigh all
+// earlier ones, so the weights are formed again on about 5% of steps. The
+// first step takes its reference max from the (masked) scores of the first
+// two steps before forming its weights, so neither forms them twice.
+#include "prefill_f32_block.hpp"
 #include "wrs_internal.hpp"
 
 #include <type_traits>
@@ -190,6 +198,9 @@ template <typename T>
 __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, int n_qblk) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kNB * kTileH];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kNB * kTileH];
+  __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
+  static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Ks), "f32 tiles fit in the K buffers");
+  static_assert(kThreads == f32blk::kThreads && kM == 2 * f32blk::kM, "two f32 blocks");
 
   const int lid = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
   const int qblk = lid % n_qblk;
@@ -201,6 +212,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hl = lane >> 5;
+  // Cleared before the first tile barrier; set only after the last one.
+  if (tid == 0) nonfinite = 0;
 
   const T* qp = static_cast<const T*>(a.q) + b * a.lq.bs + h * a.lq.hs;
   const T* kp = static_cast<const T*>(a.k) + b * a.lk.bs + h * a.lk.hs;
@@ -389,12 +402,17 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   auto settle = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
     bool need = false;
 #pragma unroll
-    // Unsigned compare of the bit patterns: true for sums above the limit,
-    // inf and NaN alike (the kernel is built without NaN semantics, so a
-    // float compare may not see NaN). Row sums are never negative.
+    // Unsigned compares of the bit patterns: true for sums above the limit or
+    // above the earlier steps' sum, inf and NaN alike (the kernel is built
+    // without NaN semantics, so a float compare may not see NaN). Row sums are
+    // never negative.
+    // 2 * l by its exponent field (l is finite, and 0 before the first step).
     for (int j = 0; j < kQB; ++j)
-      need |= __builtin_bit_cast(uint32_t, ls[j][0]) > __builtin_bit_cast(uint32_t, kSumLimit);
+      need |= __builtin_bit_cast(uint32_t, ls[j][0]) >
+              min(__builtin_bit_cast(uint32_t, l[j]) + 0x00800000u,
+                  __builtin_bit_cast(uint32_t, kSumLimit));
     if (__builtin_amdgcn_ballot_w64(need)) {
+      bool moved = false;
 #pragma unroll
       for (int j = 0; j < kQB; ++j) {
         float mr = fmaxf(s[j][0], s[j][1]);
@@ -407,10 +425,13 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
           l[j] *= alpha;
           o[j][0] *= alpha;
           o[j][1] *= alpha;
+          moved = true;
         }
       }
-      weights(s, pb);
-      row_sums(pb, ls);
+      if (__builtin_amdgcn_ballot_w64(moved)) {
+        weights(s, pb);
+        row_sums(pb, ls);
+      }
     }
 #pragma unroll
     for (int j = 0; j < kQB; ++j) l[j] += ls[j][0];
@@ -446,13 +467,20 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       if (kFull || j + 1 < nh) qk(ka, s_out);
       if (!kFull && j >= first_masked) mask_step(j, s_in);
       if (!kFull && j == 0) {
-        // First step: take the reference max from the (masked) scores now, so
-        // the weights are formed once instead of being redone by the rescale.
+        // First step: take the reference max from the (masked) scores of the
+        // first two steps now (those of step 1 were just issued above), so the
+        // weights of both are formed against their exact max and once.
+        const bool two = nh > 1;
+        if (two && 1 >= first_masked) mask_step(1, s_out);
 #pragma unroll
         for (int jb = 0; jb < kQB; ++jb) {
           float mr = fmaxf(s_in[jb][0], s_in[jb][1]);
 #pragma unroll
           for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s_in[jb][i]), s_in[jb][i + 1]);
+          if (two) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s_out[jb][i]), s_out[jb][i + 1]);
+          }
           const float mx = pair_max(mr) * c;
           if (mx > m[jb]) m[jb] = mx;
         }
@@ -517,6 +545,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     pv(va, pbb);  // last step (odd): weights in pbb
   }
 
+  // Sum of this lane's stored outputs: inf/NaN when any of them is.
+  float chk = 0.f;
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
     // l is the whole row sum in both lanes of the query (the row sums are).
@@ -525,13 +555,37 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(q0 + 32 * j) * a.lo.rs;
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        *reinterpret_cast<f32x4*>(op + 8 * gq + 4 * hl) =
+        const f32x4 lo4 =
             f32x4{o[j][0][4 * gq], o[j][0][4 * gq + 1], o[j][0][4 * gq + 2], o[j][0][4 * gq + 3]} *
             inv;
-        *reinterpret_cast<f32x4*>(op + 32 + 8 * gq + 4 * hl) =
+        const f32x4 hi4 =
             f32x4{o[j][1][4 * gq], o[j][1][4 * gq + 1], o[j][1][4 * gq + 2], o[j][1][4 * gq + 3]} *
             inv;
+        *reinterpret_cast<f32x4*>(op + 8 * gq + 4 * hl) = lo4;
+        *reinterpret_cast<f32x4*>(op + 32 + 8 * gq + 4 * hl) = hi4;
+        if constexpr (Elem<T>::kConvertV)
+          chk += (lo4[0] + lo4[1]) + (lo4[2] + lo4[3]) + (hi4[0] + hi4[1]) + (hi4[2] + hi4[3]);
       }
+    }
+  }
+  if constexpr (Elem<T>::kConvertV) {
+    // A bf16 V value of magnitude >= 65536 is inf after the f16 conversion and
+    // turns the rows that meet it into inf/NaN (a finite sum that overflows
+    // only costs a needless recompute). Then the whole workgroup recomputes its
+    // 256 queries from the bf16 inputs with the f32 block routine, in LDS
+    // that the tiles no longer use. This file is built without NaN semantics,
+    // under which isfinite, and a bit test the compiler recognizes as one,
+    // become |x| == inf (false for NaN): the exponent bits are tested as an
+    // integer that the compiler cannot trace to a float.
+    uint32_t chk_bits = __builtin_bit_cast(uint32_t, chk);
+    asm volatile("" : "+v"(chk_bits));
+    const bool bad = (chk_bits & 0x7f800000u) == 0x7f800000u;
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) nonfinite = 1;
+    __syncthreads();
+    if (nonfinite) {
+      auto& tl = *reinterpret_cast<f32blk::Tiles<2>*>(Ks);
+      f32blk::fa2_block<__bf16, __bf16, 2>(a, 2 * qblk, h, b, tl);
+      f32blk::fa2_block<__bf16, __bf16, 2>(a, 2 * qblk + 1, h, b, tl);
     }
   }
 }
