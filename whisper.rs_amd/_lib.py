@@ -6,11 +6,14 @@ entry point raises instead of computing anything on the CPU.
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
-LIB_PATH = PKG_DIR / "lib" / "libwrs_attn.so"
+# WRS_ATTN_LIB selects another build of the library (same C ABI); by default
+# the one built in the package's lib/ directory.
+LIB_PATH = Path(os.environ.get("WRS_ATTN_LIB") or PKG_DIR / "lib" / "libwrs_attn.so")
 HEADER_PATH = PKG_DIR.parent / "include" / "wrs_attn.h"
 
 WRS_OK = 0

@@ -136,16 +136,32 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   const int col = lane & 15, kg = lane >> 4;
   const bool lo_part = col >= 8;
 
-  // q rows of the group, staged once per workgroup: thread t < rows*16 loads
-  // 4 values (row t/16), scales them by scale*log2(e) and by the power of two
-  // that puts the row's largest magnitude into [2^14, 2^15), and stores them.
-  __shared__ __attribute__((aligned(16))) float qs[8][64];
+  // q * scale * log2(e), scaled per row by the power of two that puts the
+  // row's largest magnitude into [2^14, 2^15). Groups of several rows (the
+  // beams of a cross decode) stage it once per workgroup: thread t < rows*16
+  // loads 4 values of row t/16 and stores them scaled in LDS. A one-row group
+  // (a self-decode slot) has each lane load its own 16 values instead: the
+  // staging barrier would hold back the workgroup's waves, which for short
+  // sequences finish their keys soon after the loads land.
+  constexpr bool kStageQ = rows > 1;
+  const int qrow = col & 7;
+  __shared__ __attribute__((aligned(16))) float qs[kStageQ ? 8 : 1][64];
   __shared__ float qdown[8];
-  const bool qload = tid < rows * 16;
+  const bool qload = kStageQ && tid < rows * 16;
   f32x4 qx = {0.f, 0.f, 0.f, 0.f};
-  if (qload)
-    qx = *reinterpret_cast<const f32x4*>(a.q + static_cast<int64_t>(g * rows + (tid >> 4)) * a.q_rs +
-                                         h * 64 + 4 * (tid & 15));
+  float qv[16];
+  if constexpr (kStageQ) {
+    if (qload)
+      qx = *reinterpret_cast<const f32x4*>(a.q + static_cast<int64_t>(g * rows + (tid >> 4)) *
+                                                     a.q_rs + h * 64 + 4 * (tid & 15));
+  } else {
+    const float* qp = a.q + static_cast<int64_t>(g) * a.q_rs + h * 64 + 8 * kg;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qv[j] = qp[j];
+      qv[8 + j] = qp[32 + j];
+    }
+  }
   // Lane (col, kg) carries key kbase + col: d 8kg..8kg+7 and 32+8kg.. of its
   // K and V rows (the A-operand layout of a 16x16x32 MFMA).
   const int kbase = split * kChunk + wave * 16;
@@ -165,26 +181,23 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   // arithmetic below depends on a value defined after them.
   float one;
   __asm__ volatile("v_mov_b32 %0, 1.0" : "=v"(one) : : "memory");
-  if (qload) {
-    qx *= a.scale_log2 * one;
-    float amax = fmaxf(fmaxf(fabsf(qx[0]), fabsf(qx[1])), fmaxf(fabsf(qx[2]), fabsf(qx[3])));
-    amax = fmaxf(amax, dpp<0xB1>(amax));   // the row's 16 lanes (DPP inside a row)
-    amax = fmaxf(amax, dpp<0x4E>(amax));
-    amax = fmaxf(amax, dpp<0x141>(amax));
-    amax = fmaxf(amax, dpp<0x140>(amax));
-    const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
-    const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
-    *reinterpret_cast<f32x4*>(&qs[tid >> 4][4 * (tid & 15)]) = qx * pow2(sh);
-    if ((tid & 15) == 0) qdown[tid >> 4] = pow2(clamp_exp(-sh));
-  }
-  __syncthreads();
-
-  // Split into f16 high (columns 0-7 of B) and low (columns 8-15) parts; rows
-  // past the group's are zero.
-  const int qrow = col & 7;
-  const float down = qrow < rows ? qdown[qrow] : 1.f;
-  float qv[16];
-  {
+  float down;
+  if constexpr (kStageQ) {
+    if (qload) {
+      qx *= a.scale_log2 * one;
+      float amax = fmaxf(fmaxf(fabsf(qx[0]), fabsf(qx[1])), fmaxf(fabsf(qx[2]), fabsf(qx[3])));
+      amax = fmaxf(amax, dpp<0xB1>(amax));  // the row's 16 lanes (DPP inside a row)
+      amax = fmaxf(amax, dpp<0x4E>(amax));
+      amax = fmaxf(amax, dpp<0x141>(amax));
+      amax = fmaxf(amax, dpp<0x140>(amax));
+      const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+      const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
+      *reinterpret_cast<f32x4*>(&qs[tid >> 4][4 * (tid & 15)]) = qx * pow2(sh);
+      if ((tid & 15) == 0) qdown[tid >> 4] = pow2(clamp_exp(-sh));
+    }
+    __syncthreads();
+    // Rows past the group's are zero.
+    down = qrow < rows ? qdown[qrow] : 1.f;
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     const f32x4 q0 = qrow < rows ? *reinterpret_cast<const f32x4*>(&qs[qrow][8 * kg]) : z4;
     const f32x4 q1 = qrow < rows ? *reinterpret_cast<const f32x4*>(&qs[qrow][8 * kg + 4]) : z4;
@@ -197,7 +210,24 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
       qv[8 + j] = q2[j];
       qv[12 + j] = q3[j];
     }
+  } else {
+    // The one row sits in the B columns col == 0 (high) and 8 (low).
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      qv[j] = (qrow == 0 ? qv[j] : 0.f) * (a.scale_log2 * one);
+      amax = fmaxf(amax, fabsf(qv[j]));
+    }
+    amax = max_x16_x32(amax);
+    const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xFF);
+    const int sh = e_max == 0 ? 0 : clamp_exp(141 - e_max);
+    const float up = pow2(sh);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) qv[j] *= up;
+    down = pow2(clamp_exp(-sh));
   }
+
+  // Split into f16 high (columns 0-7 of B) and low (columns 8-15) parts.
   f16x8 b0, b1;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
