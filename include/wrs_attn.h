@@ -130,7 +130,10 @@ int wrs_mha_with_cache(wrs_attn_ctx *ctx, const float *q, size_t q_len, const fl
  * in {F16, BF16} (d_head 64 runs on the 16-bit MFMA kernel, other d_head on
  * the f32 one), and q F32 with kv F32/F16/BF16 (f32 accumulate-check kernel).
  * d_head <= 128. 16-bit tensors need 16-byte aligned rows (strides multiple
- * of 8 elements). */
+ * of 8 elements). The 16-bit kernel forms the PV product in f16: for bf16
+ * inputs, a workgroup whose outputs come out inf/NaN (a V value of magnitude
+ * >= 65536) recomputes its queries with f32 operands in the same launch, so
+ * any finite bf16 input gives a finite, f32-accurate result. */
 int wrs_attn_prefill(wrs_attn_ctx *ctx, int q_dtype, const void *q, const wrs_layout *q_layout,
                      int kv_dtype, const void *k, const wrs_layout *k_layout, const void *v,
                      const wrs_layout *v_layout, float *out, const wrs_layout *out_layout,
