@@ -28,6 +28,14 @@ def ctx(wrs):
     return c
 
 
+@pytest.fixture(params=[128, 256], ids=["wg128", "wg256"])
+def schedule(request, monkeypatch):
+    """Both workgroup sizes of the 16-bit kernel on the same shapes: small grids
+    normally take 128-query workgroups, large ones 256."""
+    monkeypatch.setenv("WRS_PREFILL_QUERIES", str(request.param))
+    return request.param
+
+
 def _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal=False):
     out = np.zeros(t_q * d_model, np.float32)
     orc.flash_attention_2(np.ascontiguousarray(q.ravel()), np.ascontiguousarray(k.ravel()),
@@ -131,7 +139,7 @@ def test_tiny_encoder_f32(wrs, orc, ctx):
     assert maxerr(out[0], ref) <= TOL32
 
 
-def test_base_encoder_f16(wrs, orc, ctx):
+def test_base_encoder_f16(wrs, orc, ctx, schedule):
     from wrs_amd import workloads as W
     cfg = W.BASE_ENCODER
     note(f"device prefill f16 MFMA: {cfg.name}")
@@ -142,7 +150,7 @@ def test_base_encoder_f16(wrs, orc, ctx):
         assert maxerr(out[w], ref) <= TOL16, f"window {w}"
 
 
-def test_large_encoder_bf16(wrs, orc, ctx):
+def test_large_encoder_bf16(wrs, orc, ctx, schedule):
     from wrs_amd import workloads as W
     cfg = W.LARGE_ENCODER
     note(f"device prefill bf16 MFMA: {cfg.name}")
@@ -168,10 +176,11 @@ def test_large_encoder_bf16(wrs, orc, ctx):
 
 
 @pytest.mark.parametrize("t", [1000, 1500])
-def test_prefill_many_query_blocks(wrs, ctx, t):
+def test_prefill_many_query_blocks(wrs, ctx, t, schedule):
     # Several rounds of workgroups (640 query blocks): every window of the
-    # batch equals the same window run alone, bitwise, and matches the
-    # float64 reference.
+    # batch equals the same window run alone, bitwise (with the workgroup size
+    # fixed: the two sizes round differently), and matches the float64
+    # reference.
     from wrs_amd import workloads as W
     B, H = 40, 4
     dm = H * 64
@@ -226,7 +235,7 @@ RAGGED = [(1, 1), (1, 1500), (37, 63), (128, 64), (129, 65), (300, 257), (64, 15
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("t_q,t_kv", RAGGED)
-def test_prefill_ragged_shapes(wrs, orc, ctx, dtype, t_q, t_kv):
+def test_prefill_ragged_shapes(wrs, orc, ctx, dtype, t_q, t_kv, schedule):
     from wrs_amd import workloads as W
     H = 3
     dm = H * 64
@@ -245,7 +254,7 @@ def test_prefill_ragged_shapes(wrs, orc, ctx, dtype, t_q, t_kv):
 
 @pytest.mark.parametrize("t_q,t_kv,offset", [(5, 12, 7), (100, 137, 37), (128, 448, 320),
                                              (90, 33, 0), (168, 37, 0)])
-def test_prefill_causal_with_offset(wrs, ctx, t_q, t_kv, offset):
+def test_prefill_causal_with_offset(wrs, ctx, t_q, t_kv, offset, schedule):
     from wrs_amd import workloads as W
     H = 2
     dm = H * 64
@@ -287,7 +296,7 @@ BOUNDARY_TKV = [31, 32, 33, 95, 96, 160, 191, 192, 193, 255, 256, 257, 320, 577]
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("t_kv", BOUNDARY_TKV)
-def test_prefill_tile_boundaries(wrs, ctx, dtype, t_kv):
+def test_prefill_tile_boundaries(wrs, ctx, dtype, t_kv, schedule):
     # 1..10 key tiles, partial last steps, and three query workgroups (t_q 600)
     from wrs_amd import workloads as W
     H, t_q = 2, 600
@@ -307,7 +316,7 @@ def test_prefill_tile_boundaries(wrs, ctx, dtype, t_kv):
 
 @pytest.mark.parametrize("t_q,t_kv,offset", [(600, 600, 0), (513, 700, 187), (260, 1500, 1240),
                                              (300, 64, 0), (257, 257, 0)])
-def test_prefill_causal_workgroups(wrs, ctx, t_q, t_kv, offset):
+def test_prefill_causal_workgroups(wrs, ctx, t_q, t_kv, offset, schedule):
     # causal masks across several query workgroups, first tiles masked or not
     from wrs_amd import workloads as W
     H = 2
@@ -439,7 +448,7 @@ def _bf16_run(wrs, ctx, q, k, v, B, H, T):
     return host(out)
 
 
-def test_bf16_v_beyond_f16_range(wrs, orc, ctx):
+def test_bf16_v_beyond_f16_range(wrs, orc, ctx, schedule):
     # The 16-bit kernel widens bf16 V to f16 in LDS; |v| >= 65536 has no f16
     # value. Those blocks come out non-finite, are listed, and are recomputed by
     # the f32 kernel from the bf16 inputs, so the result is finite and matches

@@ -49,6 +49,7 @@
 #include "prefill_f32_block.hpp"
 #include "wrs_internal.hpp"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace wrs {
@@ -66,10 +67,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr int kQB = 2;              // 32-query blocks per wave
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kM = 64 * kWaves;     // queries per workgroup
 constexpr int kN = 64;              // keys per tile
 constexpr int kNB = 4;              // LDS tile buffers
 constexpr int kTileH = kN * 64;     // 16-bit elements per K (or V) tile: 8 KiB
@@ -191,16 +190,24 @@ __device__ inline void wait_tiles() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-typedef f32x16 SBlk[kQB];
-typedef u32x4 PBlk[kQB][2];
+// QB: 32-query blocks per wave (2, or 1 for grids below one round of
+// workgroups); a workgroup holds 32 * QB * kWaves queries.
+template <int QB>
+constexpr int queries_per_wg() {
+  return 32 * QB * kWaves;
+}
 
-template <typename T>
+template <typename T, int QB>
 __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, int n_qblk) {
+  constexpr int kQB = QB;
+  constexpr int kM = queries_per_wg<QB>();
+  typedef f32x16 SBlk[kQB];
+  typedef u32x4 PBlk[kQB][2];
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kNB * kTileH];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kNB * kTileH];
   __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
   static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Ks), "f32 tiles fit in the K buffers");
-  static_assert(kThreads == f32blk::kThreads && kM == 2 * f32blk::kM, "two f32 blocks");
+  static_assert(kThreads == f32blk::kThreads && kM % f32blk::kM == 0, "whole f32 blocks");
 
   const int lid = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
   const int qblk = lid % n_qblk;
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const T* vp = static_cast<const T*>(a.v) + b * a.lv.bs + h * a.lv.hs;
 
   // This lane's queries: column r32 of each of the wave's S^T blocks.
-  const int q0 = qblk * kM + wave * 64 + r32;
+  const int q0 = qblk * kM + wave * (32 * kQB) + r32;
   u32x4 qf[kQB][4];
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
@@ -494,19 +501,19 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
         // 16 S/PV MFMAs spread over the softmax, then the 4 row-sum MFMAs
         // (they need the last weights), with the LDS reads in between.
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 4 * kQB; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);    // DS read
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 4 * kQB; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2 * kQB; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
         }
@@ -572,7 +579,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     // A bf16 V value of magnitude >= 65536 is inf after the f16 conversion and
     // turns the rows that meet it into inf/NaN (a finite sum that overflows
     // only costs a needless recompute). Then the whole workgroup recomputes its
-    // 256 queries from the bf16 inputs with the f32 block routine, in LDS
+    // queries from the bf16 inputs with the f32 block routine, in LDS
     // that the tiles no longer use. This file is built without NaN semantics,
     // under which isfinite, and a bit test the compiler recognizes as one,
     // become |x| == inf (false for NaN): the exponent bits are tested as an
@@ -584,10 +591,34 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     __syncthreads();
     if (nonfinite) {
       auto& tl = *reinterpret_cast<f32blk::Tiles<2>*>(Ks);
-      f32blk::fa2_block<__bf16, __bf16, 2>(a, 2 * qblk, h, b, tl);
-      f32blk::fa2_block<__bf16, __bf16, 2>(a, 2 * qblk + 1, h, b, tl);
+      constexpr int kBlocks = kM / f32blk::kM;
+      f32blk::fa2_block<__bf16, __bf16, 2>(a, kBlocks * qblk, h, b, tl);
+      if constexpr (kBlocks == 2) f32blk::fa2_block<__bf16, __bf16, 2>(a, 2 * qblk + 1, h, b, tl);
     }
   }
+}
+
+// Resident 256-thread workgroups of this kernel on the current device (two per
+// CU), read once.
+int64_t small_grid_limit() {
+  static const int64_t limit = [] {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    return static_cast<int64_t>(2) * cus;
+  }();
+  return limit;
+}
+
+template <int QB>
+hipError_t launch_qb(const PrefillArgs& a, DType dt, int64_t nwg, int n_qblk, hipStream_t s) {
+  if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads);
+  if (dt == kF16)
+    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB>), grid, block, 0, s, a, n_qblk);
+  else
+    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB>), grid, block, 0, s, a, n_qblk);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -603,16 +634,23 @@ bool prefill_mfma16_supports(const PrefillArgs& a) {
 
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) {
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
-  const int n_qblk = (a.t_q + kM - 1) / kM;
-  const int64_t nwg = static_cast<int64_t>(n_qblk) * a.n_heads * a.batch;
-  if (nwg <= 0) return hipSuccess;
-  if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads);
-  if (dt == kF16)
-    hipLaunchKernelGGL(fa2_prefill_d64<_Float16>, grid, block, 0, s, a, n_qblk);
-  else
-    hipLaunchKernelGGL(fa2_prefill_d64<__bf16>, grid, block, 0, s, a, n_qblk);
-  return hipGetLastError();
+  // 256-query workgroups, unless that grid fills less than one round of the
+  // device's resident slots (two per CU): then 128-query workgroups, so more
+  // CUs run two workgroups (two waves per SIMD issue the softmax VALU work
+  // about twice as fast as one).
+  constexpr int kM2 = queries_per_wg<2>(), kM1 = queries_per_wg<1>();
+  const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
+  const int n_qblk2 = (a.t_q + kM2 - 1) / kM2;
+  const int64_t nwg2 = n_qblk2 * bh;
+  if (nwg2 <= 0) return hipSuccess;
+  // WRS_PREFILL_QUERIES=128 or 256 forces one schedule (tests, measurements).
+  const char* force = std::getenv("WRS_PREFILL_QUERIES");
+  const int forced = force ? std::atoi(force) : 0;
+  if (forced == kM1 || (forced != kM2 && nwg2 < small_grid_limit())) {
+    const int n_qblk1 = (a.t_q + kM1 - 1) / kM1;
+    return launch_qb<1>(a, dt, n_qblk1 * bh, n_qblk1, s);
+  }
+  return launch_qb<2>(a, dt, nwg2, n_qblk2, s);
 }
 
 }  // namespace wrs
