@@ -51,6 +51,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;            // exact f32 decode
 constexpr int kRedPitch = 68;            // LDS pitch (floats) of a wave's 16 output rows
+constexpr int kQsPitch = 68;             // LDS pitch (floats) of the staged q rows
 constexpr int kPart = 68;    // floats per partial row: m, l, 2 pad, acc[64]
 constexpr int kCounterStride = 32;  // 128 bytes between merge counters
 constexpr int kRawBuffer = 0x00020000;  // buffer resource word 3: raw, 32-bit data format
@@ -146,7 +147,9 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   // sequences finish their keys soon after the loads land.
   constexpr bool kStageQ = rows > 1;
   const int qrow = col & 7;
-  __shared__ __attribute__((aligned(16))) float qs[kStageQ ? 8 : 1][64];
+  // Rows padded to 68 floats: the 8 rows read at one column fall in distinct
+  // banks (at a 64-float pitch they shared them).
+  __shared__ __attribute__((aligned(16))) float qs[kStageQ ? 8 : 1][kQsPitch];
   __shared__ float qdown[8];
   const bool qload = kStageQ && tid < rows * 16;
   f32x4 qx = {0.f, 0.f, 0.f, 0.f};
