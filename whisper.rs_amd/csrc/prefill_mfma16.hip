@@ -455,7 +455,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     tile_barrier();
 
     SBlk sa, sb;
-    PBlk pa, pbb;
+    PBlk pb;
     u32x4 ka[4];
     u32x2 va[8];
     f32x4 ls[kQB];
@@ -468,9 +468,10 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     // then the lazy-rescale check of step j. Full steps have every part and
     // no mask, so their body is one basic block, interleaved as groups of one
     // MFMA and a few VALU instructions.
-    auto step = [&](auto full_tag, int j, SBlk& s_in, SBlk& s_out, PBlk& p_out,
-                    PBlk& p_in) __attribute__((always_inline)) {
+    auto step = [&](auto full_tag, int j, SBlk& s_in, SBlk& s_out) __attribute__((always_inline)) {
       constexpr bool kFull = decltype(full_tag)::value;
+      // P V of step j-1 first: its weights' registers are then free for step j's.
+      if (kFull || j >= 1) pv(va, pb);
       if (kFull || j + 1 < nh) qk(ka, s_out);
       if (!kFull && j >= first_masked) mask_step(j, s_in);
       if (!kFull && j == 0) {
@@ -492,9 +493,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
           if (mx > m[jb]) m[jb] = mx;
         }
       }
-      weights(s_in, p_out);
-      row_sums(p_out, ls);
-      if (kFull || j >= 1) pv(va, p_in);
+      weights(s_in, pb);
+      row_sums(pb, ls);
       if (kFull || j + 2 < nh) kfetch(j + 2, ka);
       vfetch(j, va);
       if constexpr (kFull) {
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      settle(s_in, p_out, ls);
+      settle(s_in, pb, ls);
       __builtin_amdgcn_sched_barrier(0);
     };
     typedef std::integral_constant<bool, true> Full;
@@ -531,8 +531,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     auto tile = [&](auto full_tag, int t) __attribute__((always_inline)) {
       const bool more = t + 3 < n_tiles;
       if (more) issue_tile(t + 3);
-      step(full_tag, 2 * t, sa, sb, pa, pbb);
-      step(full_tag, 2 * t + 1, sb, sa, pbb, pa);
+      step(full_tag, 2 * t, sa, sb);
+      step(full_tag, 2 * t + 1, sb, sa);
       if (t + 2 < n_tiles && t > 0) {
         if (more)
           wait_tiles<4>();
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     int t = 1;
     for (; t < t_full_end; ++t) tile(Full{}, t);
     for (; t < n_tiles; ++t) tile(Part{}, t);
-    pv(va, pbb);  // last step (odd): weights in pbb
+    pv(va, pb);  // the last step's weights
   }
 
   // Sum of this lane's stored outputs: inf/NaN when any of them is.
