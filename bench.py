@@ -330,8 +330,14 @@ def bench_decode_self(wrs, W, ctx, reps, lengths=None, eager=False):
     return res
 
 
-def bench_capture(wrs, W, ctx, reps, use_graph=True):
-    """DTW alignment pass: one capture launch per preset layer, inputs resident."""
+def bench_capture(wrs, W, ctx, reps, use_graph=True, one_pass=True):
+    """DTW alignment pass: one capture call per preset layer, inputs resident.
+
+    one_pass: each layer's capture reads the row statistics that the layer's
+    cross-attention over the same rows left (decoder.rs:698-721's order; that
+    attention call, made once before timing, is the decoder's own work and not
+    timed here): one launch per call. Otherwise the two-pass capture of the
+    reference-shaped entry point, which computes its own statistics."""
     import torch
     cfg = W.LARGE_DTW_CAPTURE
     layers = cfg.layers()
@@ -342,10 +348,17 @@ def bench_capture(wrs, W, ctx, reps, use_graph=True):
     qs = {layer: torch.from_numpy(cfg.q(layer)).cuda() for layer in layers}
     n_sel = len(cfg.heads)
     out = torch.zeros(cfg.n_tokens * n_sel * cfg.n_audio, device="cuda")
+    lse = {}
+    if one_pass:
+        att = torch.zeros((cfg.n_tokens, cfg.d_model), device="cuda")
+        for layer in layers:
+            lse[layer] = torch.zeros(2 * cfg.n_heads * cfg.n_tokens, device="cuda")
+            ar.prefill_cross(layer, qs[layer], att, lse=lse[layer])
 
     def all_layers():
         for layer in layers:
-            ar.capture_cross_heads(layer, qs[layer], cfg.pairs(layer), n_sel, 0, out)
+            ar.capture_cross_heads(layer, qs[layer], cfg.pairs(layer), n_sel, 0, out,
+                                   lse=lse.get(layer))
 
     all_layers()
     torch.cuda.synchronize()
@@ -370,7 +383,8 @@ def bench_capture(wrs, W, ctx, reps, use_graph=True):
         g.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    log(f"capture: timing {reps} graph replays of {len(layers)} launches")
+    log(f"capture ({'one pass' if one_pass else 'two passes'}): timing {reps} graph replays "
+        f"of {len(layers)} calls")
     start.record()
     for _ in range(reps):
         g.replay()
@@ -663,7 +677,9 @@ TRAFFIC_LEGS = {
     "encoder_base": (r"fa2_prefill_d64(?:<\s*|I)(?:_Float16|half|DF16_)", None),
     "decode": (r"decode_f16<\s*5\s*,", None),
     "decode_self": (r"decode_f16<\s*1\s*,", None),
-    "capture": (r"capture_cross", None),
+    # capture_cross_f16<2> is the one-pass kernel, <0> and <1> the two passes
+    "capture": (r"capture_cross_f16(?:<\s*|ILi)2", None),
+    "capture_two_pass": (r"capture_cross_f16(?:<\s*|ILi)[01]", None),
     "linear": (r"linear_f16w", None),
     "stream": (r"gemv_f16w", "per_step"),
 }
@@ -741,6 +757,7 @@ def run_traffic_legs(wrs, W, ctx):
     bench_decode(wrs, W, ctx, 3, use_graph=False)
     bench_decode_self(wrs, W, ctx, 3, lengths=(W.SMALL_SELF_DECODE.ctx,), eager=True)
     bench_capture(wrs, W, ctx, 3, use_graph=False)
+    bench_capture(wrs, W, ctx, 3, use_graph=False, one_pass=False)
     bench_linear(wrs, W.LARGE_QKV_F16, ctx, 3, settle=False)
     bench_weight_stream(wrs, W, ctx, TRAFFIC_STREAM_STEPS, eager=True)
     calibration_copy()
@@ -967,8 +984,11 @@ def main():
         return
     if args.only == "capture":
         _, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps, use_graph=not args.eager)
+        _, cus2, cgbs2 = bench_capture(wrs, W, ctx, args.capture_reps, use_graph=not args.eager,
+                                       one_pass=False)
         calibration_copy()
-        log(f"capture only: {cus:.3f} us/launch, {cgbs:.1f} GB/s")
+        log(f"capture only: one pass {cus:.3f} us/call, {cgbs:.1f} GB/s; two passes "
+            f"{cus2:.3f} us/call, {cgbs2:.1f} GB/s")
         return
 
     cfg, ms, tflops, qkv, settled = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
@@ -977,6 +997,7 @@ def main():
     dcfg, us, gbs, floor = bench_decode(wrs, W, ctx, args.decode_reps)
     sweep = bench_decode_self(wrs, W, ctx, args.decode_reps)
     ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
+    _, cus2, cgbs2 = bench_capture(wrs, W, ctx, args.capture_reps, one_pass=False)
     lcfg = W.LARGE_QKV_F16
     lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
     lms32, ltf32 = bench_linear(wrs, W.LARGE_QKV_F32, ctx, args.linear_reps)
@@ -1067,6 +1088,10 @@ def main():
             "us_per_launch": round(cus, 3), "launches_per_step": len(ccfg.layers()),
             "bytes_per_launch": ccfg.bytes_per_pair(), "dtype": "f32",
             "roofline": _roof(cgbs, PEAK_HBM_GBS, "GB/s", "hbm", traffic_bytes("capture")),
+            "mode": "one launch per call, on the row statistics of the layer's cross-attention",
+            "two_pass": {"us_per_call": round(cus2, 3), "GBps": round(cgbs2, 1),
+                         "roofline": _roof(cgbs2, PEAK_HBM_GBS, "GB/s", "hbm",
+                                           traffic_bytes("capture_two_pass"))},
             "cpu_baseline": cpu.get("capture"),
         },
         "projection": {

@@ -219,6 +219,15 @@ int wrs_attn_prefill_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, size_t sl
                           const float *q, size_t n_tokens, float *out);
 int wrs_attn_prefill_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
                            size_t n_tokens, float *out);
+/* wrs_attn_prefill_cross (the multi_head_attention call of decoder.rs:698-708,
+ * any n_tokens >= 1, always on the f32 kernel) that also writes each row's
+ * softmax statistics for wrs_attn_capture_cross_heads_lse: lse is an f32
+ * device buffer of n_heads * n_tokens * 2 values, (max, sum) of row i of head
+ * h at 2 * (h * n_tokens + i), in the exp2 domain: max = log2(e) * max_j s_ij,
+ * sum = sum_j exp2(log2(e) * s_ij - max), s_ij = q_i.k_j / 8. Not written when
+ * the layer has no cross keys. */
+int wrs_attn_prefill_cross_lse(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
+                               size_t n_tokens, float *out, float *lse);
 
 /* ---- alignment-head capture (asynchronous) -----------------------------
  * fn capture_cross_attention_heads(q, k, n_tokens, n_audio, n_heads, d_model,
@@ -233,6 +242,18 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, co
                                  size_t n_tokens, const size_t *slots, const size_t *heads,
                                  size_t n_pairs, size_t n_selected, size_t row_offset,
                                  float *out, size_t out_len);
+/* The same capture in one launch, for the decoder's order of calls
+ * (decoder.rs:698-721: the cross-attention of the same q rows runs first):
+ * lse is what wrs_attn_prefill_cross_lse wrote for these q rows and this
+ * layer, and the weights are exp2(log2(e) * s - max) / sum with them. The
+ * statistics come from the attention kernel's own score sums, whose rounding
+ * differs from this kernel's exact-product sums: weights agree with
+ * wrs_attn_capture_cross_heads to ~1e-6 relative, rows sum to 1 within 1e-5. */
+int wrs_attn_capture_cross_heads_lse(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer,
+                                     const float *q, size_t n_tokens, const size_t *slots,
+                                     const size_t *heads, size_t n_pairs, size_t n_selected,
+                                     size_t row_offset, float *out, size_t out_len,
+                                     const float *lse);
 
 /* ---- projections with f16 weights (asynchronous) -----------------------
  * LinearWeight::linear with F16 weights (crates/tensor/src/weight.rs:116-137

@@ -152,12 +152,20 @@ pub mod ffi {
             slot: usize, q: *const f32, n_tokens: usize, out: *mut f32) -> c_int;
         pub fn wrs_attn_prefill_cross(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
             q: *const f32, n_tokens: usize, out: *mut f32) -> c_int;
+        // the same, also writing the rows' softmax statistics for the one-pass capture
+        pub fn wrs_attn_prefill_cross_lse(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
+            q: *const f32, n_tokens: usize, out: *mut f32, lse: *mut f32) -> c_int;
 
         // decoder.rs:796-828 capture_cross_attention_heads; `selected` as two arrays
         pub fn wrs_attn_capture_cross_heads(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
             q: *const f32, n_tokens: usize, slots: *const usize, heads: *const usize,
             n_pairs: usize, n_selected: usize, row_offset: usize, out: *mut f32,
             out_len: usize) -> c_int;
+        // one launch, with the statistics wrs_attn_prefill_cross_lse wrote for the same rows
+        pub fn wrs_attn_capture_cross_heads_lse(ctx: *mut WrsCtx, kv: *mut WrsKv, layer: usize,
+            q: *const f32, n_tokens: usize, slots: *const usize, heads: *const usize,
+            n_pairs: usize, n_selected: usize, row_offset: usize, out: *mut f32,
+            out_len: usize, lse: *const f32) -> c_int;
 
         // weight.rs:116-137 / quant.rs:415-473: LinearWeight::linear with f16 weights
         pub fn wrs_linear(ctx: *mut WrsCtx, x_dtype: c_int, x: *const c_void, x_len: usize,
@@ -383,6 +391,37 @@ impl<'c> KvArena<'c> {
                                        out: *mut f32) {
         self.ctx.check(wrs_attn_decode_cross_noalloc(self.ctx.raw(), self.kv, layer, q,
                                                      n_beams, out));
+    }
+    /// decoder.rs:698-708's cross-attention of `n_tokens` prompt rows, also
+    /// writing the rows' softmax statistics for [`KvArena::capture_cross_heads_lse`].
+    ///
+    /// # Safety
+    /// `q` and `out` are device pointers of `n_tokens * d_model` f32, `lse` of
+    /// `2 * n_heads * n_tokens` f32.
+    pub unsafe fn prefill_cross_lse(&self, layer: usize, q: *const f32, n_tokens: usize,
+                                    out: *mut f32, lse: *mut f32) {
+        self.ctx.check(wrs_attn_prefill_cross_lse(self.ctx.raw(), self.kv, layer, q, n_tokens,
+                                                  out, lse));
+    }
+    /// decoder.rs:709-721's alignment-head capture in one launch, from the
+    /// statistics `prefill_cross_lse` wrote for the same rows; `selected` holds
+    /// (slot, head) pairs as the reference's `layer_heads` does.
+    ///
+    /// # Safety
+    /// `q` is a device pointer of `n_tokens * d_model` f32, `out` of `out_len` f32,
+    /// `lse` as written by `prefill_cross_lse` for these rows.
+    #[allow(clippy::too_many_arguments)]
+    pub unsafe fn capture_cross_heads_lse(&self, layer: usize, q: *const f32, n_tokens: usize,
+                                          selected: &[(usize, usize)], n_selected: usize,
+                                          row_offset: usize, out: *mut f32, out_len: usize,
+                                          lse: *const f32) {
+        let slots: Vec<usize> = selected.iter().map(|&(s, _)| s).collect();
+        let heads: Vec<usize> = selected.iter().map(|&(_, h)| h).collect();
+        self.ctx.check(wrs_attn_capture_cross_heads_lse(self.ctx.raw(), self.kv, layer, q,
+                                                        n_tokens, slots.as_ptr(),
+                                                        heads.as_ptr(), selected.len(),
+                                                        n_selected, row_offset, out, out_len,
+                                                        lse));
     }
 }
 

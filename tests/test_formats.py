@@ -83,6 +83,9 @@ def test_traffic_patterns_match_mangled_and_demangled_names():
                          "void wrs::(anonymous namespace)::fa2_prefill_d64<_Float16>(wrs::PrefillArgs, int)"],
         "decode": ["void wrs::(anonymous namespace)::decode_f16<5, 8>(wrs::DecodeArgs)"],
         "decode_self": ["void wrs::(anonymous namespace)::decode_f16<1, 16>(wrs::DecodeArgs)"],
+        "capture": ["void wrs::(anonymous namespace)::capture_cross_f16<2>(wrs::CaptureArgs, int, int)"],
+        "capture_two_pass": ["void wrs::(anonymous namespace)::capture_cross_f16<0>(wrs::CaptureArgs, int, int)",
+                             "_ZN3wrs12_GLOBAL__N_117capture_cross_f16ILi1EEEvNS_11CaptureArgsEii"],
     }
     for leg, ns in names.items():
         for n in ns:

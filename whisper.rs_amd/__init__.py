@@ -436,10 +436,21 @@ class KvArena:
                                                 q.data_ptr(), q.shape[0], out.data_ptr()),
                 "prefill_self")
 
-    def prefill_cross(self, layer, q, out):
-        self._c(self._lib.wrs_attn_prefill_cross(self.ctx.handle, self.handle, layer,
-                                                 q.data_ptr(), q.shape[0], out.data_ptr()),
-                "prefill_cross")
+    def prefill_cross(self, layer, q, out, lse=None):
+        """Cross-attention of prompt rows (decoder.rs:698-708). With ``lse`` (a
+        float32 device tensor of n_heads * n_tokens * 2 values) the rows' softmax
+        statistics are written too, for ``capture_cross_heads(..., lse=lse)``."""
+        if lse is None:
+            self._c(self._lib.wrs_attn_prefill_cross(self.ctx.handle, self.handle, layer,
+                                                     q.data_ptr(), q.shape[0], out.data_ptr()),
+                    "prefill_cross")
+            return
+        import torch
+        assert lse.dtype == torch.float32 and lse.numel() >= 2 * self.n_heads * q.shape[0]
+        self._c(self._lib.wrs_attn_prefill_cross_lse(self.ctx.handle, self.handle, layer,
+                                                     q.data_ptr(), q.shape[0], out.data_ptr(),
+                                                     lse.data_ptr()),
+                "prefill_cross_lse")
 
     def set_cross_proj(self, enc, w_k, w_v, b_v=None):
         """precompute_cross_attn (crates/whisper/src/decoder.rs:423-447) into the
@@ -457,16 +468,24 @@ class KvArena:
                                                 wv, bv),
                 "set_cross_proj")
 
-    def capture_cross_heads(self, layer, q, selected, n_selected, row_offset, out):
+    def capture_cross_heads(self, layer, q, selected, n_selected, row_offset, out, lse=None):
         """capture_cross_attention_heads (crates/whisper/src/decoder.rs:796-828).
 
         ``selected`` lists this layer's (slot, head) pairs; ``q`` is the
         layer's [n_tokens][d_model] float32 query tensor and ``out`` the float32
         capture buffer laid out [row][slot][n_audio] (decoder.rs:821-822).
+        With ``lse`` (from ``prefill_cross(..., lse=...)`` on the same rows and
+        layer) the capture is one launch instead of two.
         """
         n = len(selected)
         slots = (ctypes.c_size_t * max(n, 1))(*[s for s, _ in selected])
         heads = (ctypes.c_size_t * max(n, 1))(*[h for _, h in selected])
-        self._c(self._lib.wrs_attn_capture_cross_heads(
+        if lse is None:
+            self._c(self._lib.wrs_attn_capture_cross_heads(
+                self.ctx.handle, self.handle, layer, q.data_ptr(), q.shape[0], slots, heads, n,
+                n_selected, row_offset, out.data_ptr(), out.numel()), "capture_cross_heads")
+            return
+        self._c(self._lib.wrs_attn_capture_cross_heads_lse(
             self.ctx.handle, self.handle, layer, q.data_ptr(), q.shape[0], slots, heads, n,
-            n_selected, row_offset, out.data_ptr(), out.numel()), "capture_cross_heads")
+            n_selected, row_offset, out.data_ptr(), out.numel(), lse.data_ptr()),
+            "capture_cross_heads_lse")

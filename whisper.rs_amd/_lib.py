@@ -91,6 +91,7 @@ _SIGNATURES = {
     "wrs_attn_decode_cross_noalloc": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_self": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "wrs_attn_prefill_cross": (_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "wrs_attn_prefill_cross_lse": (_int, [_vp, _vp, _sz, _vp, _sz, _vp, _vp]),
     "wrs_linear": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _vp, _vp, _sz, _sz, _sz, _int,
                           _vp, _sz, ctypes.c_int64, ctypes.c_int64]),
     "wrs_linear_group": (_int, [_vp, _int, _vp, _sz, ctypes.c_int64, _sz, ctypes.POINTER(_vp),
@@ -106,6 +107,8 @@ _SIGNATURES = {
                                      ctypes.POINTER(_vp)]),
     "wrs_attn_capture_cross_heads": (_int, [_vp, _vp, _sz, _vp, _sz, _szp, _szp, _sz, _sz, _sz,
                                             _vp, _sz]),
+    "wrs_attn_capture_cross_heads_lse": (_int, [_vp, _vp, _sz, _vp, _sz, _szp, _szp, _sz, _sz, _sz,
+                                            _vp, _sz, _vp]),
 }
 
 _lib = None

@@ -2,8 +2,11 @@
 // (replaces crates/whisper/src/decoder.rs:796-828 capture_cross_attention_heads,
 //  called per text layer from decoder.rs:709-721 for DTW word timestamps).
 //
-// K5 (capture_cross_f16<pass>): grid (key chunk, query block, pair), two
-//   launches of the same kernel. A workgroup of 4 waves owns 16 query rows of
+// K5 (capture_cross_f16<pass>): one workgroup per (query block, key chunk,
+//   pair), ordered so that the query blocks of one key chunk run on one XCD and
+//   share its L2. Two launches of the same kernel, or one when the attention
+//   pass over the same q and keys left its row statistics (pass 2 below). A
+//   workgroup of 4 waves owns 16 query rows of
 //   one (slot, head) pair and one chunk of 128 keys of that head's f16 cross
 //   plane (wave w: key tiles 2w and 2w+1 of 16 keys). Splitting the keys over
 //   workgroups is what makes this fast: one CU streams only ~40 GB/s, so a
@@ -24,6 +27,11 @@
 //   exp2(s - M) * (1 / L): the max / exp / sum / reciprocal-multiply of
 //   softmax.rs:1-23 with the sum gathered per chunk. Each lane stores the 4
 //   consecutive weights of its query column as one 16-byte write.
+//   Pass 2 is pass 1 with the row's (M, L) read from the statistics the
+//   attention kernel wrote for the same rows (wrs_attn_prefill_cross_lse):
+//   those come from its own f32 score sums, whose order differs from this
+//   kernel's exact-product sums, so weights agree with the two-pass ones to
+//   ~1e-6 relative rather than bit for bit.
 #include "wrs_internal.hpp"
 
 namespace wrs {
@@ -51,16 +59,29 @@ __device__ inline f32x4 mfma16(const u32x4& a, const f16x8& b, const f32x4& c) {
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
 __device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
 
+// Workgroup p of a launch runs on XCD p mod 8; consecutive work items should
+// share an XCD, so item = the p-th of that XCD's share.
+__device__ inline int xcd_remap(int pid, int nwg) {
+  const int xcd = pid & 7, k = pid >> 3;
+  const int per = nwg >> 3, rem = nwg & 7;
+  return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
+}
+
 template <int kPass>
-__global__ __launch_bounds__(kThreads) void capture_cross_f16(CaptureArgs a) {
+__global__ __launch_bounds__(kThreads) void capture_cross_f16(CaptureArgs a, int n_blocks,
+                                                               int n_chunks) {
   __shared__ float red[kWaves][kRows];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15;  // query column of this lane (B operand, C column)
   const int g = lane >> 4;  // k-group of the operands; keys 4g..4g+3 of a C tile
-  const int chunk = blockIdx.x, n_chunks = gridDim.x;
-  const int block = blockIdx.y, pair = blockIdx.z;
+  // Work item = block + n_blocks * (chunk + n_chunks * pair): the query blocks
+  // of one chunk are consecutive items, hence on one XCD.
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int block = item % n_blocks;
+  const int chunk = (item / n_blocks) % n_chunks;
+  const int pair = item / (n_blocks * n_chunks);
   const int head = a.head[pair];
   const int row = block * kRows + n;
   const bool row_ok = row < a.n_tokens;
@@ -69,10 +90,13 @@ __global__ __launch_bounds__(kThreads) void capture_cross_f16(CaptureArgs a) {
 
   // Chunk statistics of block `block`: [row in block][chunk] (max, sum).
   f32x2* stats = reinterpret_cast<f32x2*>(a.part) +
-                 (static_cast<int64_t>(pair) * gridDim.y + block) * kRows * n_chunks;
+                 (static_cast<int64_t>(pair) * n_blocks + block) * kRows * n_chunks;
   // Pass 1: the first kMergeBatch statistics of this lane's row, loaded before
   // anything else so their latency hides behind the score computation.
   f32x2 sv[kMergeBatch];
+  f32x2 row_ml = {-INFINITY, 0.0f};
+  if (kPass == 2 && row_ok)
+    row_ml = reinterpret_cast<const f32x2*>(a.lse)[static_cast<int64_t>(head) * a.n_tokens + row];
   if (kPass == 1) {
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j)
@@ -183,10 +207,10 @@ __global__ __launch_bounds__(kThreads) void capture_cross_f16(CaptureArgs a) {
   }
 
   // Pass 1: merge the row's chunk statistics (batches beyond the first fold in
-  // online), write the normalized weights.
+  // online), write the normalized weights. Pass 2: the row's statistics as given.
   if (!row_ok) return;
-  float M = -INFINITY, L = 0.0f;
-  for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
+  float M = row_ml.x, L = row_ml.y;
+  for (int c0 = 0; kPass == 1 && c0 < n_chunks; c0 += kMergeBatch) {
     if (c0 > 0) {
 #pragma unroll
       for (int j = 0; j < kMergeBatch; ++j)
@@ -232,12 +256,19 @@ size_t capture_part_floats(int n_pairs, int n_tokens, int n_audio) {
 
 hipError_t launch_capture_cross_f16(const CaptureArgs& a, hipStream_t s) {
   if (a.n_tokens <= 0 || a.n_pairs <= 0 || a.n_audio <= 0) return hipSuccess;
-  dim3 grid((a.n_audio + kChunkKeys - 1) / kChunkKeys, (a.n_tokens + kRows - 1) / kRows,
-            a.n_pairs);
-  hipLaunchKernelGGL(capture_cross_f16<0>, grid, dim3(kThreads), 0, s, a);
+  const int n_chunks = (a.n_audio + kChunkKeys - 1) / kChunkKeys;
+  const int n_blocks = (a.n_tokens + kRows - 1) / kRows;
+  const int64_t items = static_cast<int64_t>(n_chunks) * n_blocks * a.n_pairs;
+  if (items > 0x7fffffff) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(items));
+  if (a.lse) {
+    hipLaunchKernelGGL(capture_cross_f16<2>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(capture_cross_f16<0>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(capture_cross_f16<1>, grid, dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL(capture_cross_f16<1>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks);
   return hipGetLastError();
 }
 

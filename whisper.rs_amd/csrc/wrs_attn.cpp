@@ -187,10 +187,14 @@ int run_exact(wrs_attn_ctx* c, const float* q, size_t q_floats, const float* k, 
   return WRS_OK;
 }
 
+// lse (optional): per-row softmax statistics, [batch][head][t_q][2] f32 in the
+// exp2 domain; only the f32 kernel writes them, so a call that asks for them
+// always runs there.
 int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& lq, int kv_dtype,
                  const void* k, const wrs_layout& lk, const void* v, const wrs_layout& lv,
                  float* out, const wrs_layout& lo, size_t batch, size_t n_heads, size_t t_q,
-                 size_t t_kv, size_t d_head, int causal, size_t q_pos_offset) {
+                 size_t t_kv, size_t d_head, int causal, size_t q_pos_offset,
+                 float* lse = nullptr) {
   if (batch == 0 || n_heads == 0 || t_q == 0) return WRS_OK;
   if (!q || !out || (t_kv && (!k || !v))) return fail(c, WRS_EINVAL, "null tensor pointer");
   if (d_head == 0 || d_head > 128) return fail(c, WRS_EUNSUPPORTED, "d_head must be 1..128");
@@ -219,6 +223,7 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
   a.causal = causal ? 1 : 0;
   a.q_pos_offset = static_cast<int>(q_pos_offset);
   a.scale = 1.0f / std::sqrt(static_cast<float>(d_head));
+  a.lse = lse;
 
   if (t_kv == 0) {
     // attention.rs:93-96: zero output. Rows of out may be strided.
@@ -233,7 +238,7 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && l.batch_stride % mult == 0 &&
            l.head_stride % mult == 0 && l.row_stride % mult == 0;
   };
-  if (same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
+  if (!lse && same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
       aligned16(v, lv, 8) && aligned16(out, lo, 4) && wrs::prefill_mfma16_supports(a)) {
     WRS_HIP(c, wrs::launch_prefill_mfma16(a, q_dtype == WRS_F16 ? wrs::kF16 : wrs::kBF16,
                                           c->stream));
@@ -1013,10 +1018,30 @@ int wrs_attn_prefill_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const floa
                       n_tokens, kv->cross_len[layer], 64, 0, 0);
 }
 
-int wrs_attn_capture_cross_heads(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
-                                 size_t n_tokens, const size_t* slots, const size_t* heads,
-                                 size_t n_pairs, size_t n_selected, size_t row_offset, float* out,
-                                 size_t out_len) {
+int wrs_attn_prefill_cross_lse(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                               size_t n_tokens, float* out, float* lse) {
+  if (!c || !kv) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n_tokens == 0) return WRS_OK;
+  if (!lse) return fail(c, WRS_EINVAL, "null lse");
+  DeviceGuard g(c->device);
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  const wrs_layout lq{0, 64, dm};
+  const wrs_layout lkv{0, static_cast<int64_t>(kv->n_audio_max * 64), 64};
+  const uint16_t* kb = kv->k_cross + kv->cross_off(layer);
+  const uint16_t* vb = kv->v_cross + kv->cross_off(layer);
+  return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
+                      n_tokens, kv->cross_len[layer], 64, 0, 0, lse);
+}
+
+}  // extern "C"
+
+namespace {
+
+int capture_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, size_t n_tokens,
+                 const size_t* slots, const size_t* heads, size_t n_pairs, size_t n_selected,
+                 size_t row_offset, float* out, size_t out_len, const float* lse) {
   if (!c || !kv) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
   if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
@@ -1052,12 +1077,15 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, cons
   a.n_selected = static_cast<int>(n_selected);
   a.row_offset = static_cast<int>(row_offset);
   a.scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) (decoder.rs:810) * log2(e)
-  const size_t pb =
-      wrs::capture_part_floats(static_cast<int>(std::min<size_t>(n_pairs, wrs::kMaxCapturePairs)),
-                               a.n_tokens, a.n_audio) * sizeof(float);
-  int rc = grow(c, reinterpret_cast<void**>(&c->cap_part), &c->cap_part_bytes, pb, false);
-  if (rc) return rc;
-  a.part = c->cap_part;
+  a.lse = lse;
+  if (!lse) {  // two passes: chunk statistics in the context
+    const size_t pb =
+        wrs::capture_part_floats(static_cast<int>(std::min<size_t>(n_pairs, wrs::kMaxCapturePairs)),
+                                 a.n_tokens, a.n_audio) * sizeof(float);
+    int rc = grow(c, reinterpret_cast<void**>(&c->cap_part), &c->cap_part_bytes, pb, false);
+    if (rc) return rc;
+    a.part = c->cap_part;
+  }
   for (size_t p0 = 0; p0 < n_pairs; p0 += wrs::kMaxCapturePairs) {
     const size_t np = std::min<size_t>(wrs::kMaxCapturePairs, n_pairs - p0);
     a.n_pairs = static_cast<int>(np);
@@ -1068,6 +1096,31 @@ int wrs_attn_capture_cross_heads(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, cons
     WRS_HIP(c, wrs::launch_capture_cross_f16(a, c->stream));
   }
   return WRS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wrs_attn_capture_cross_heads(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                                 size_t n_tokens, const size_t* slots, const size_t* heads,
+                                 size_t n_pairs, size_t n_selected, size_t row_offset, float* out,
+                                 size_t out_len) {
+  return capture_impl(c, kv, layer, q, n_tokens, slots, heads, n_pairs, n_selected, row_offset,
+                      out, out_len, nullptr);
+}
+
+int wrs_attn_capture_cross_heads_lse(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
+                                     size_t n_tokens, const size_t* slots, const size_t* heads,
+                                     size_t n_pairs, size_t n_selected, size_t row_offset,
+                                     float* out, size_t out_len, const float* lse) {
+  if (!lse) {
+    if (!c) return WRS_EINVAL;
+    std::lock_guard<std::mutex> lk(c->mu);
+    return fail(c, WRS_EINVAL, "null lse");
+  }
+  return capture_impl(c, kv, layer, q, n_tokens, slots, heads, n_pairs, n_selected, row_offset,
+                      out, out_len, lse);
 }
 
 }  // extern "C"

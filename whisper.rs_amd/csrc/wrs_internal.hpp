@@ -46,6 +46,10 @@ struct PrefillArgs {
   int causal;        // mask keys j > i + q_pos_offset
   int q_pos_offset;  // absolute position of query row 0 (decoder prompt: t_past)
   float scale;       // 1/sqrt(d_head), rounded to f32 like attention.rs:107
+  // f32 kernel only: when set, row i of head h of batch entry b writes its
+  // softmax statistics (row max in the exp2 domain, sum of exp2(x - max)) at
+  // lse[2 * ((b * n_heads + h) * t_q + i)].
+  float* lse;
 };
 
 // MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type, rows 16-byte
@@ -121,6 +125,10 @@ struct CaptureArgs {
   int64_t q_rs, kv_hs;
   int n_tokens, n_audio, n_selected, row_offset, n_pairs;
   float scale_log2;  // log2(e)/sqrt(64): decoder.rs:810's scale in the exp2 domain
+  // When set: per-row softmax statistics of the attention pass over the same q
+  // and keys, (max, sum) in the exp2 domain at lse[2 * (head * n_tokens + row)];
+  // the capture then runs as one pass.
+  const float* lse;
   int slot[kMaxCapturePairs];
   int head[kMaxCapturePairs];
 };
