@@ -349,11 +349,33 @@ def bench_capture(wrs, W, ctx, reps, use_graph=True, one_pass=True):
     n_sel = len(cfg.heads)
     out = torch.zeros(cfg.n_tokens * n_sel * cfg.n_audio, device="cuda")
     lse = {}
+    rows_us = float("nan")
     if one_pass:
         att = torch.zeros((cfg.n_tokens, cfg.d_model), device="cuda")
         for layer in layers:
             lse[layer] = torch.zeros(2 * cfg.n_heads * cfg.n_tokens, device="cuda")
             ar.prefill_cross(layer, qs[layer], att, lse=lse[layer])
+        torch.cuda.synchronize()
+        if use_graph:
+            # the decoder's own cross-attention of the same rows (its output and
+            # the statistics), timed on its own: decoder.rs:698-708 per layer
+            ga = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(ga):
+                ctx.use_torch_stream()
+                for layer in layers:
+                    ar.prefill_cross(layer, qs[layer], att, lse=lse[layer])
+            ctx.use_torch_stream()
+            for _ in range(3):
+                ga.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                ga.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            rows_us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+            log(f"capture: the layers' cross-attention of the {cfg.n_tokens} rows with "
+                f"statistics: {rows_us:.2f} us per layer")
 
     def all_layers():
         for layer in layers:
@@ -393,6 +415,7 @@ def bench_capture(wrs, W, ctx, reps, use_graph=True, one_pass=True):
     us = start.elapsed_time(end) * 1e3 / (reps * len(layers))
     gbs = cfg.bytes_per_pair() / (us * 1e-6) / 1e9  # one pair per preset layer
     ar.close()
+    bench_capture.rows_us = rows_us
     return cfg, us, gbs
 
 
@@ -997,6 +1020,7 @@ def main():
     dcfg, us, gbs, floor = bench_decode(wrs, W, ctx, args.decode_reps)
     sweep = bench_decode_self(wrs, W, ctx, args.decode_reps)
     ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
+    cross_rows_us = bench_capture.rows_us
     _, cus2, cgbs2 = bench_capture(wrs, W, ctx, args.capture_reps, one_pass=False)
     lcfg = W.LARGE_QKV_F16
     lms, ltf = bench_linear(wrs, lcfg, ctx, args.linear_reps)
@@ -1089,6 +1113,7 @@ def main():
             "bytes_per_launch": ccfg.bytes_per_pair(), "dtype": "f32",
             "roofline": _roof(cgbs, PEAK_HBM_GBS, "GB/s", "hbm", traffic_bytes("capture")),
             "mode": "one launch per call, on the row statistics of the layer's cross-attention",
+            "cross_attention_rows_us_per_layer": round(cross_rows_us, 2),
             "two_pass": {"us_per_call": round(cus2, 3), "GBps": round(cgbs2, 1),
                          "roofline": _roof(cgbs2, PEAK_HBM_GBS, "GB/s", "hbm",
                                            traffic_bytes("capture_two_pass"))},

@@ -214,14 +214,16 @@ int wrs_attn_decode_cross_noalloc(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, c
                                   size_t n_beams, float *out);
 /* Multi-token rows (prompt prefill): decoder.rs:857-891 self-attention with
  * offset t_past = slot_len(slot) over the slot's f16 cache (rows appended),
- * and attention.rs:107-243 cross-attention with t_q = n_tokens. */
+ * and attention.rs:107-243 cross-attention with t_q = n_tokens (the rows run
+ * on the split-K decode kernel in groups of 8 that share each read of the
+ * plane, with its numerics: f16 keys and values, q split into two f16 parts). */
 int wrs_attn_prefill_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, size_t slot,
                           const float *q, size_t n_tokens, float *out);
 int wrs_attn_prefill_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
                            size_t n_tokens, float *out);
-/* wrs_attn_prefill_cross (the multi_head_attention call of decoder.rs:698-708,
- * any n_tokens >= 1, always on the f32 kernel) that also writes each row's
- * softmax statistics for wrs_attn_capture_cross_heads_lse: lse is an f32
+/* wrs_attn_prefill_cross (the multi_head_attention call of decoder.rs:698-708)
+ * that also writes each row's softmax statistics for
+ * wrs_attn_capture_cross_heads_lse: lse is an f32
  * device buffer of n_heads * n_tokens * 2 values, (max, sum) of row i of head
  * h at 2 * (h * n_tokens + i), in the exp2 domain: max = log2(e) * max_j s_ij,
  * sum = sum_j exp2(log2(e) * s_ij - max), s_ij = q_i.k_j / 8. Not written when

@@ -89,6 +89,14 @@ __device__ inline float ld_agent(const float* p) {
 }
 
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
+
+// Row statistics for the one-pass alignment-head capture: (max, sum) in the
+// exp2 domain, the scores being q.k * scale * log2(e).
+__device__ inline void store_lse(const DecodeArgs& a, int row, int h, float m, float l) {
+  float* st = a.lse + 2 * (static_cast<int64_t>(h) * a.lse_rows + a.lse_row0 + row);
+  st[0] = m;
+  st[1] = l;
+}
 __device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
 
 // x op x[lane ^ 32] and x op x[lane ^ 16] with the gfx950 lane-swap VALU
@@ -314,8 +322,10 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
     }
   }
   if (a.n_splits == 1) {
-    if (own)
+    if (own) {
       a.o[static_cast<int64_t>(g * rows + qr) * a.o_rs + h * 64 + qd] = Lsum > 0.f ? pv * (1.f / Lsum) : 0.f;
+      if (a.lse && qd == 0) store_lse(a, g * rows + qr, h, M, Lsum);
+    }
     return;
   }
 
@@ -375,6 +385,7 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
       M = Mb;
     }
     a.o[static_cast<int64_t>(g * rows + qr) * a.o_rs + h * 64 + qd] = L > 0.f ? acc * (1.f / L) : 0.f;
+    if (a.lse && qd == 0) store_lse(a, g * rows + qr, h, M, L);
   }
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

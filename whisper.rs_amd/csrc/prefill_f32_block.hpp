@@ -134,12 +134,6 @@ __device__ inline void fa2_block(const PrefillArgs& a, int qblk, int h, int b, T
 
   l += __shfl_xor(l, 32);
   const float inv = (l > 0.f) ? 1.f / l : 0.f;
-  if (a.lse && qi < a.t_q && hl == 0) {
-    // exp(x - m) == exp2(x log2(e) - m log2(e)): the statistics in the exp2 domain
-    float* st = a.lse + 2 * ((static_cast<int64_t>(b) * a.n_heads + h) * a.t_q + qi);
-    st[0] = m * 1.4426950408889634f;
-    st[1] = l;
-  }
   if (qi < a.t_q) {
     float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(qi) * a.lo.rs;
 #pragma unroll

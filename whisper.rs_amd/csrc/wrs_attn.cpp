@@ -187,14 +187,10 @@ int run_exact(wrs_attn_ctx* c, const float* q, size_t q_floats, const float* k, 
   return WRS_OK;
 }
 
-// lse (optional): per-row softmax statistics, [batch][head][t_q][2] f32 in the
-// exp2 domain; only the f32 kernel writes them, so a call that asks for them
-// always runs there.
 int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& lq, int kv_dtype,
                  const void* k, const wrs_layout& lk, const void* v, const wrs_layout& lv,
                  float* out, const wrs_layout& lo, size_t batch, size_t n_heads, size_t t_q,
-                 size_t t_kv, size_t d_head, int causal, size_t q_pos_offset,
-                 float* lse = nullptr) {
+                 size_t t_kv, size_t d_head, int causal, size_t q_pos_offset) {
   if (batch == 0 || n_heads == 0 || t_q == 0) return WRS_OK;
   if (!q || !out || (t_kv && (!k || !v))) return fail(c, WRS_EINVAL, "null tensor pointer");
   if (d_head == 0 || d_head > 128) return fail(c, WRS_EUNSUPPORTED, "d_head must be 1..128");
@@ -223,7 +219,6 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
   a.causal = causal ? 1 : 0;
   a.q_pos_offset = static_cast<int>(q_pos_offset);
   a.scale = 1.0f / std::sqrt(static_cast<float>(d_head));
-  a.lse = lse;
 
   if (t_kv == 0) {
     // attention.rs:93-96: zero output. Rows of out may be strided.
@@ -238,7 +233,7 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && l.batch_stride % mult == 0 &&
            l.head_stride % mult == 0 && l.row_stride % mult == 0;
   };
-  if (!lse && same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
+  if (same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
       aligned16(v, lv, 8) && aligned16(out, lo, 4) && wrs::prefill_mfma16_supports(a)) {
     WRS_HIP(c, wrs::launch_prefill_mfma16(a, q_dtype == WRS_F16 ? wrs::kF16 : wrs::kBF16,
                                           c->stream));
@@ -293,7 +288,8 @@ unsigned char* noalloc_ptr(int device) {
 int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64_t o_rs,
                 const uint16_t* kbase, const uint16_t* vbase, int64_t kv_hs,
                 const std::vector<int64_t>& goff, const std::vector<int>& lens, int rows_per_group,
-                int n_heads, unsigned char* fixed = nullptr) {
+                int n_heads, unsigned char* fixed = nullptr, float* lse = nullptr,
+                int lse_rows = 0, int lse_row0 = 0) {
   const int n_groups = static_cast<int>(goff.size());
   if (n_groups == 0) return WRS_OK;
   if (!kbase || !vbase) return fail(c, WRS_EINVAL, "decode over an unallocated K/V plane");
@@ -324,6 +320,9 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
                 : wrs::kDecodeChunk;
   a.n_splits = std::max(1, (max_len + a.chunk - 1) / a.chunk);
   a.scale_log2 = 0.125f * 1.4426950408889634f;
+  a.lse = lse;
+  a.lse_rows = lse_rows;
+  a.lse_row0 = lse_row0;
   if (a.n_splits > 1) {
     const size_t pb =
         wrs::decode_part_floats(n_groups, n_heads, a.n_splits, rows_per_group) * sizeof(float);
@@ -475,16 +474,19 @@ int wrs_attn_reserve(wrs_attn_ctx* c, const wrs_reserve* r) {
   const int heads = static_cast<int>(r->n_heads);
   if (heads && r->decode_rows && r->decode_keys > static_cast<size_t>(wrs::kDecodeChunkLong)) {
     // One decode launch: groups x rows_per_group query rows (a self step's
-    // slots, up to kMaxDecodeGroups, or an utterance's beams, up to
-    // kMaxRowsPerGroup), each row's partials per split of kDecodeChunk keys.
+    // slots, up to kMaxDecodeGroups; an utterance's beams, up to
+    // kMaxRowsPerGroup; cross-attention prompt rows, up to kMaxDecodeGroups
+    // groups of kMaxRowsPerGroup), each row's partials per split of
+    // kDecodeChunk keys.
     const int rows = static_cast<int>(std::min<size_t>(
-        r->decode_rows, std::max(wrs::kMaxDecodeGroups, wrs::kMaxRowsPerGroup)));
+        r->decode_rows, static_cast<size_t>(wrs::kMaxDecodeGroups) * wrs::kMaxRowsPerGroup));
+    const int groups = std::min(rows, wrs::kMaxDecodeGroups);
     const int splits = static_cast<int>((r->decode_keys + wrs::kDecodeChunk - 1) / wrs::kDecodeChunk);
     rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes,
               wrs::decode_part_floats(rows, heads, splits, 1) * sizeof(float), false);
     if (rc) return rc;
     rc = grow(c, reinterpret_cast<void**>(&c->counters), &c->counter_bytes,
-              wrs::decode_counter_words(rows, heads) * sizeof(unsigned), true);
+              wrs::decode_counter_words(groups, heads) * sizeof(unsigned), true);
     if (rc) return rc;
   }
   if (r->capture_tokens && r->capture_keys) {
@@ -962,6 +964,44 @@ int decode_cross_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
   return WRS_OK;
 }
 
+// Cross-attention of n query rows over one layer's plane on the split-K decode
+// kernel: groups of kMaxRowsPerGroup rows share each read of the plane, up to
+// kMaxDecodeGroups groups per launch, and the remaining rows one last group.
+// With lse, the rows' statistics too ([head][n][2], exp2 domain).
+int cross_rows_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, size_t n,
+                    float* out, float* lse) {
+  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
+  if (n == 0) return WRS_OK;
+  if (!q || !out) return fail(c, WRS_EINVAL, "null argument");
+  if (!fits_int(n)) return fail(c, WRS_EINVAL, "dimension exceeds 2^31");
+  DeviceGuard g(c->device);
+  const int64_t dm = static_cast<int64_t>(kv->d_model());
+  const size_t L = kv->cross_len[layer];
+  if (L == 0) {
+    // attention.rs:93-96: no keys, zero output (the plane may not exist).
+    WRS_HIP(c, wrs::launch_fill_zero_rows(out, 0, 0, dm, 1, 1, static_cast<int>(n),
+                                          static_cast<int>(dm), c->stream));
+    return WRS_OK;
+  }
+  for (size_t r0 = 0; r0 < n;) {
+    const size_t left = n - r0;
+    const int rpg = static_cast<int>(std::min<size_t>(left, wrs::kMaxRowsPerGroup));
+    const size_t groups =
+        left >= static_cast<size_t>(wrs::kMaxRowsPerGroup)
+            ? std::min<size_t>(left / wrs::kMaxRowsPerGroup, wrs::kMaxDecodeGroups)
+            : 1;
+    std::vector<int64_t> goff(groups, static_cast<int64_t>(kv->cross_off(layer)));
+    std::vector<int> lens(groups, static_cast<int>(L));
+    int rc = decode_impl(c, q + r0 * dm, dm, out + r0 * dm, dm, kv->k_cross, kv->v_cross,
+                         static_cast<int64_t>(kv->n_audio_max * 64), goff, lens, rpg,
+                         static_cast<int>(kv->n_heads), nullptr, lse, static_cast<int>(n),
+                         static_cast<int>(r0));
+    if (rc) return rc;
+    r0 += groups * static_cast<size_t>(rpg);
+  }
+  return WRS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1004,35 +1044,16 @@ int wrs_attn_prefill_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, size_t slot
 int wrs_attn_prefill_cross(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
                            size_t n_tokens, float* out) {
   if (!c || !kv) return WRS_EINVAL;
-  if (n_tokens == 1) return wrs_attn_decode_cross(c, kv, layer, q, 1, out);
   std::lock_guard<std::mutex> lk(c->mu);
-  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
-  if (n_tokens == 0) return WRS_OK;
-  DeviceGuard g(c->device);
-  const int64_t dm = static_cast<int64_t>(kv->d_model());
-  const wrs_layout lq{0, 64, dm};
-  const wrs_layout lkv{0, static_cast<int64_t>(kv->n_audio_max * 64), 64};
-  const uint16_t* kb = kv->k_cross + kv->cross_off(layer);
-  const uint16_t* vb = kv->v_cross + kv->cross_off(layer);
-  return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
-                      n_tokens, kv->cross_len[layer], 64, 0, 0);
+  return cross_rows_impl(c, kv, layer, q, n_tokens, out, nullptr);
 }
 
 int wrs_attn_prefill_cross_lse(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
                                size_t n_tokens, float* out, float* lse) {
   if (!c || !kv) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
-  if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
-  if (n_tokens == 0) return WRS_OK;
-  if (!lse) return fail(c, WRS_EINVAL, "null lse");
-  DeviceGuard g(c->device);
-  const int64_t dm = static_cast<int64_t>(kv->d_model());
-  const wrs_layout lq{0, 64, dm};
-  const wrs_layout lkv{0, static_cast<int64_t>(kv->n_audio_max * 64), 64};
-  const uint16_t* kb = kv->k_cross + kv->cross_off(layer);
-  const uint16_t* vb = kv->v_cross + kv->cross_off(layer);
-  return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
-                      n_tokens, kv->cross_len[layer], 64, 0, 0, lse);
+  if (!lse && n_tokens) return fail(c, WRS_EINVAL, "null lse");
+  return cross_rows_impl(c, kv, layer, q, n_tokens, out, lse);
 }
 
 }  // extern "C"

@@ -46,10 +46,6 @@ struct PrefillArgs {
   int causal;        // mask keys j > i + q_pos_offset
   int q_pos_offset;  // absolute position of query row 0 (decoder prompt: t_past)
   float scale;       // 1/sqrt(d_head), rounded to f32 like attention.rs:107
-  // f32 kernel only: when set, row i of head h of batch entry b writes its
-  // softmax statistics (row max in the exp2 domain, sum of exp2(x - max)) at
-  // lse[2 * ((b * n_heads + h) * t_q + i)].
-  float* lse;
 };
 
 // MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type, rows 16-byte
@@ -97,6 +93,10 @@ struct DecodeArgs {
   float scale_log2;  // (1/8) * log2(e)
   float* part;        // scratch: [groups][heads][splits][rows][68]
   unsigned* counters;  // scratch: one per (group, head) every 32 words, zero between launches
+  // Optional: row statistics (max, sum of exp2(s - max)) of output row
+  // lse_row0 + g*rows_per_group + r for head h at lse[2 * (h * lse_rows + row)].
+  float* lse;
+  int lse_rows, lse_row0;
 };
 constexpr int kDecodeChunk = 128;
 constexpr int kDecodeChunkLong = 256;  // one workgroup per (group, head) up to this length
