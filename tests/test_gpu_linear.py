@@ -165,6 +165,59 @@ def test_linear_head_plane_layout(wrs, orc, ctx):
     assert np.isnan(got[:, n_tokens:]).all()  # rows past n_tokens untouched
 
 
+@pytest.mark.parametrize("n_tokens,n_out,pad,offset,x_dt,out_dt", [
+    (300, 260, 0, 0, "f16", torch.bfloat16),    # n_out % 8 == 4: last chunk is 8 bytes
+    (300, 264, 8, 0, "f16", torch.float16),     # 16-byte rows, padded: pad untouched
+    (513, 512, 4, 4, "f16", torch.bfloat16),    # 8-byte aligned start: 8-byte stores
+    (257, 328, 0, 0, "f32", torch.float16),     # second feature tile 72 rows; row scales
+    (323, 1284, 12, 0, "f32", torch.bfloat16),  # 6 feature tiles, 2 token tiles
+])
+def test_linear_16bit_output_edges(wrs, ctx, n_tokens, n_out, pad, offset, x_dt, out_dt):
+    """16-bit output leaves the tile as whole token rows: the values equal the
+    same launch's f32 output rounded to the output type, bit for bit (one
+    accumulation, one rounding), at every alignment and partial edge, and
+    nothing outside the written range changes."""
+    note(f"linear 16-bit edges T={n_tokens} N={n_out} pad={pad} off={offset} x={x_dt} {out_dt}")
+    n_in = 192
+    rng = np.random.default_rng(n_tokens + n_out)
+    xh = rng.standard_normal((n_tokens, n_in)).astype(np.float32)
+    x = torch.from_numpy(xh if x_dt == "f32" else xh.astype(np.float16)).cuda()
+    w = torch.from_numpy(_weights(n_out, n_in, n_out)).cuda()
+    b = dev(rng.standard_normal(n_out).astype(np.float32))
+    ref = torch.full((n_tokens, n_out), float("nan"), device="cuda")
+    wrs.linear(x, w, b, ref, ctx=ctx)
+    rs = n_out + pad
+    buf = torch.full((offset + (n_tokens + 2) * rs,), float("nan"), dtype=out_dt, device="cuda")
+    out = buf[offset:]
+    wrs.linear(x, w, b, out, out_row_stride=rs, ctx=ctx)
+    torch.cuda.synchronize()
+    got = out[:n_tokens * rs].view(n_tokens, rs)
+    want = ref.to(out_dt)
+    assert torch.equal(got[:, :n_out].view(torch.int16), want.view(torch.int16))
+    assert torch.isnan(got[:, n_out:].float()).all()
+    assert torch.isnan(out[n_tokens * rs:].float()).all()
+    assert torch.isnan(buf[:offset].float()).all()
+
+
+def test_linear_16bit_head_planes(wrs, ctx):
+    """16-bit output into [head][token][64] planes (the arena layout): equal to
+    the same launch's f32 output rounded, rows past n_tokens untouched."""
+    note("linear 16-bit head planes")
+    n_tokens, n_in, n_out, plane_rows = 300, 128, 320, 304
+    rng = np.random.default_rng(77)
+    x = torch.from_numpy(rng.standard_normal((n_tokens, n_in)).astype(np.float16)).cuda()
+    w = torch.from_numpy(_weights(n_out, n_in, 78)).cuda()
+    ref = torch.full((n_out // 64, plane_rows, 64), float("nan"), device="cuda")
+    wrs.linear(x, w, None, ref, out_row_stride=64, out_head_stride=plane_rows * 64, ctx=ctx)
+    out = torch.full((n_out // 64, plane_rows, 64), float("nan"), dtype=torch.float16,
+                     device="cuda")
+    wrs.linear(x, w, None, out, out_row_stride=64, out_head_stride=plane_rows * 64, ctx=ctx)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :n_tokens].view(torch.int16),
+                       ref[:, :n_tokens].half().view(torch.int16))
+    assert torch.isnan(out[:, n_tokens:].float()).all()
+
+
 def test_linear_argument_errors(wrs, ctx):
     note("linear argument errors")
     w = torch.zeros((64, 96), dtype=torch.float16, device="cuda")

@@ -27,10 +27,13 @@
 //   weight column k' mod n_in; each product carries at most that 2^-22
 //   relative error, below what one f32 addition of the accumulation
 //   (dot_f16_f32, simd.rs:593-700) already rounds away. The epilogue multiplies by
-//   the row's 2^-shift (exact), adds the f32 bias and stores 4 consecutive
-//   features per lane in the output type, at
-//   out + t * out_rs + (r / 64) * out_hs + r % 64: token-major rows
-//   (out_hs = 64) or the arena's [head][token][64] planes.
+//   the row's 2^-shift (exact), adds the f32 bias and writes the output type
+//   at out + t * out_rs + (r / 64) * out_hs + r % 64: token-major rows
+//   (out_hs = 64) or the arena's [head][token][64] planes. A 16-bit tile
+//   passes through the freed stage buffers first and leaves as whole 512-byte
+//   token rows, 16 bytes per lane: stored straight from the MFMA layout (8
+//   bytes of 32 different rows per instruction) the same bytes took 2.2x as
+//   long to write. f32 output is stored straight from the MFMA layout.
 #include "wrs_internal.hpp"
 
 #include <algorithm>
@@ -139,9 +142,10 @@ __device__ inline void tile_of(int pid, int n_fm, int n_tn, int& fm, int& tn) {
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 lds_a[kStages * kStageA];
-  __shared__ __attribute__((aligned(16))) _Float16 lds_b[kStages * kStageB];
+  __shared__ __attribute__((aligned(16))) _Float16 lds_ab[kStages * (kStageA + kStageB)];
   __shared__ __attribute__((aligned(16))) float bias_s[kBM];  // this tile's bias
+  _Float16* const lds_a = lds_ab;
+  _Float16* const lds_b = lds_ab + kStages * kStageA;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -252,28 +256,95 @@ __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
   // of token n0 + 64 wn + 32 j + orow.
   OutT* out = reinterpret_cast<OutT*>(a.out[grp]);
   const float* bias = a.bias[grp];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = n0 + wn * 64 + j * 32 + orow;
-    if (t >= a.n_tokens) continue;
-    const float rs = a.row_scale ? a.row_scale[t] : 1.0f;
-    OutT* orow_p = out + static_cast<int64_t>(t) * a.out_rs;
+  if constexpr (sizeof(OutT) == 2) {
+    // 16-bit output: the tile goes through LDS (the stage buffers, 128 KB:
+    // 256 token rows of 512 bytes, 16-byte chunk c of row t at c ^ (t % 32)),
+    // then leaves as whole rows: 64 lanes store 2 rows of 512 bytes.
+    char* ot = reinterpret_cast<char*>(lds_a);  // lds_a and lds_b are one 128 KB span
+    // this lane's 64 bias values, read before any LDS write of the tile, so
+    // that no read waits behind the writes
+    f32x4 bv[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int r = m0 + wm * 128 + i * 32 + 8 * g + 4 * kgrp;
-        if (r >= a.n_out) continue;
-        f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                   acc[i][j][4 * g + 3]};
-        v *= rs;
-        if (bias) v += *reinterpret_cast<const f32x4*>(&bias_s[r - m0]);
-        if (a.act == kActGelu) {
+      for (int g = 0; g < 4; ++g)
+        bv[i][g] = bias ? *reinterpret_cast<const f32x4*>(&bias_s[wm * 128 + i * 32 + 8 * g + 4 * kgrp])
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();                             // every wave is done with the last stage
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+    for (int j = 0; j < 2; ++j) {
+      const int tl = wn * 64 + j * 32 + orow;
+      const int t = n0 + tl;
+      const float rs = (a.row_scale && t < a.n_tokens) ? a.row_scale[t] : 1.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int fl = wm * 128 + i * 32 + 8 * g + 4 * kgrp;  // feature within the tile
+          f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                     acc[i][j][4 * g + 3]};
+          v *= rs;
+          v += bv[i][g];
+          if (a.act == kActGelu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+          }
+          u32x2 h;
+          if constexpr (__is_same(OutT, __bf16)) {
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            h = __builtin_bit_cast(u32x2, __builtin_convertvector(v, bf16x4));
+          } else {
+            typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+            h = __builtin_bit_cast(u32x2, __builtin_convertvector(v, f16x4));
+          }
+          const int chunk = (fl >> 3) ^ (tl & 31);
+          *reinterpret_cast<u32x2*>(ot + tl * 512 + chunk * 16 + (fl & 4) * 2) = h;
         }
-        store4<OutT>(orow_p + static_cast<int64_t>(r >> 6) * a.out_hs + (r & 63), v);
+    }
+    __syncthreads();
+    const bool v16 = ((reinterpret_cast<uintptr_t>(out) | (a.out_rs * 2) | (a.out_hs * 2)) & 15) == 0;
+    const int c = lane & 31;  // 16-byte chunk: features 8c .. 8c + 7 of the row
+    const int r = m0 + 8 * c;
+    OutT* ocol = out + static_cast<int64_t>(r >> 6) * a.out_hs + (r & 63);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int tl = wave * 32 + 2 * q + (lane >> 5);
+      const int t = n0 + tl;
+      const u32x4 h = *reinterpret_cast<const u32x4*>(ot + tl * 512 + ((c ^ (tl & 31)) * 16));
+      if (t < a.n_tokens && r < a.n_out) {
+        OutT* p = ocol + static_cast<int64_t>(t) * a.out_rs;
+        if (v16 && r + 8 <= a.n_out) {
+          *reinterpret_cast<u32x4*>(p) = h;
+        } else {
+          *reinterpret_cast<u32x2*>(p) = u32x2{h[0], h[1]};
+          if (r + 8 <= a.n_out) *reinterpret_cast<u32x2*>(p + 4) = u32x2{h[2], h[3]};
+        }
       }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = n0 + wn * 64 + j * 32 + orow;
+      if (t >= a.n_tokens) continue;
+      const float rs = a.row_scale ? a.row_scale[t] : 1.0f;
+      OutT* orow_p = out + static_cast<int64_t>(t) * a.out_rs;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = m0 + wm * 128 + i * 32 + 8 * g + 4 * kgrp;
+          if (r >= a.n_out) continue;
+          f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                     acc[i][j][4 * g + 3]};
+          v *= rs;
+          if (bias) v += *reinterpret_cast<const f32x4*>(&bias_s[r - m0]);
+          if (a.act == kActGelu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+          }
+          store4<OutT>(orow_p + static_cast<int64_t>(r >> 6) * a.out_hs + (r & 63), v);
+        }
+    }
   }
 }
 
