@@ -103,25 +103,6 @@ __device__ inline void stage_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <typename OutT>
-__device__ inline void store4(OutT* p, const f32x4& v);
-template <>
-__device__ inline void store4<float>(float* p, const f32x4& v) {
-  *reinterpret_cast<f32x4*>(p) = v;
-}
-template <>
-__device__ inline void store4<_Float16>(_Float16* p, const f32x4& v) {
-  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-  const f16x4 h = __builtin_convertvector(v, f16x4);
-  *reinterpret_cast<u32x2*>(p) = __builtin_bit_cast(u32x2, h);
-}
-template <>
-__device__ inline void store4<__bf16>(__bf16* p, const f32x4& v) {
-  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-  const bf16x4 h = __builtin_convertvector(v, bf16x4);
-  *reinterpret_cast<u32x2*>(p) = __builtin_bit_cast(u32x2, h);
-}
-
 // Physical workgroup id -> tile. The hardware hands linear ids round-robin to
 // the 8 XCDs; each XCD is given a contiguous range of logical ids instead, and
 // logical ids walk groups of kGroupM feature tiles with the token tiles
@@ -342,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void linear_f16w(LinearArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
           }
-          store4<OutT>(orow_p + static_cast<int64_t>(r >> 6) * a.out_hs + (r & 63), v);
+          *reinterpret_cast<f32x4*>(orow_p + static_cast<int64_t>(r >> 6) * a.out_hs + (r & 63)) = v;
         }
     }
   }

@@ -552,27 +552,54 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     pv(va, pb);  // the last step's weights
   }
 
-  // Sum of this lane's stored outputs: inf/NaN when any of them is.
+  // The outputs leave as whole 256-byte query rows. Each wave stages its
+  // 32*QB rows in the LDS tiles (no longer read after the last tile barrier,
+  // and every tile load has landed), 16-byte chunk c of row r at c ^ (r % 16),
+  // then 16 lanes store one row: stored straight from the MFMA layout, one
+  // instruction would write 32 bytes to each of 32 rows.
+  constexpr int kStageBytes = 32 * kQB * 256;
+  static_assert(kWaves * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
+  char* const stage = wave * kStageBytes < static_cast<int>(sizeof(Ks))
+                          ? reinterpret_cast<char*>(Ks) + wave * kStageBytes
+                          : reinterpret_cast<char*>(Vs) + (wave * kStageBytes - sizeof(Ks));
+  // Sum of this lane's outputs: inf/NaN when any of them is.
   float chk = 0.f;
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
     // l is the whole row sum in both lanes of the query (the row sums are).
     const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
-    if (q0 + 32 * j < a.t_q) {
-      float* op = a.o + b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(q0 + 32 * j) * a.lo.rs;
+    const int rr = 32 * j + r32;  // row within the wave's block
+    char* const srow = stage + rr * 256;
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const f32x4 lo4 =
-            f32x4{o[j][0][4 * gq], o[j][0][4 * gq + 1], o[j][0][4 * gq + 2], o[j][0][4 * gq + 3]} *
-            inv;
-        const f32x4 hi4 =
-            f32x4{o[j][1][4 * gq], o[j][1][4 * gq + 1], o[j][1][4 * gq + 2], o[j][1][4 * gq + 3]} *
-            inv;
-        *reinterpret_cast<f32x4*>(op + 8 * gq + 4 * hl) = lo4;
-        *reinterpret_cast<f32x4*>(op + 32 + 8 * gq + 4 * hl) = hi4;
-        if constexpr (Elem<T>::kConvertV)
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 lo4 =
+          f32x4{o[j][0][4 * gq], o[j][0][4 * gq + 1], o[j][0][4 * gq + 2], o[j][0][4 * gq + 3]} *
+          inv;
+      const f32x4 hi4 =
+          f32x4{o[j][1][4 * gq], o[j][1][4 * gq + 1], o[j][1][4 * gq + 2], o[j][1][4 * gq + 3]} *
+          inv;
+      *reinterpret_cast<f32x4*>(srow + (((2 * gq + hl) ^ (rr & 15)) * 16)) = lo4;
+      *reinterpret_cast<f32x4*>(srow + (((8 + 2 * gq + hl) ^ (rr & 15)) * 16)) = hi4;
+      if constexpr (Elem<T>::kConvertV) {
+        if (q0 + 32 * j < a.t_q)
           chk += (lo4[0] + lo4[1]) + (lo4[2] + lo4[3]) + (hi4[0] + hi4[1]) + (hi4[2] + hi4[3]);
       }
+    }
+  }
+  // The wave reads back what its own lanes wrote: LDS operations of one wave
+  // complete in order.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  {
+    const int c16 = lane & 15;
+    const int qw = qblk * kM + wave * (32 * kQB);  // the wave's first query
+    float* const ob = a.o + b * a.lo.bs + h * a.lo.hs + 4 * c16;
+#pragma unroll
+    for (int k = 0; k < 8 * kQB; ++k) {
+      const int rr = 4 * k + (lane >> 4);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(stage + rr * 256 + ((c16 ^ (rr & 15)) * 16));
+      if (qw + rr < a.t_q) *reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(qw + rr) * a.lo.rs) = v;
     }
   }
   if constexpr (Elem<T>::kConvertV) {
