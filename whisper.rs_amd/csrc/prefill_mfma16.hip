@@ -599,7 +599,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     for (int k = 0; k < 8 * kQB; ++k) {
       const int rr = 4 * k + (lane >> 4);
       const f32x4 v = *reinterpret_cast<const f32x4*>(stage + rr * 256 + ((c16 ^ (rr & 15)) * 16));
-      if (qw + rr < a.t_q) *reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(qw + rr) * a.lo.rs) = v;
+      // Non-temporal: the output is not read again by this launch, and
+      // streaming it past the caches keeps them for the K/V that the other
+      // query blocks of each head still read.
+      if (qw + rr < a.t_q)
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(qw + rr) * a.lo.rs));
     }
   }
   if constexpr (Elem<T>::kConvertV) {
