@@ -117,6 +117,31 @@ def test_self_decode_sweep(wrs, orc, ctx, L):
     arena.close()
 
 
+def test_self_decode_ragged_in_one_chunk(wrs, ctx):
+    # Longest slot 256: every (slot, head) runs one 256-key workgroup whose
+    # second tiles lie past the shorter slots' lengths, or partly inside them.
+    from wrs_amd import workloads as W
+    note("device decode_self ragged lengths 1..256 (256-key workgroups)")
+    H, dm = 3, 192
+    lens = [1, 100, 128, 129, 143, 200, 255, 256]
+    arena = wrs.KvArena(1, len(lens), H, 448, 0, ctx=ctx)
+    data = []
+    for s, L in enumerate(lens):
+        k = W.normal((L, dm), 150 + s, storage="f16")
+        v = W.normal((L, dm), 170 + s, storage="f16")
+        data.append((k, v))
+        _fill_slot(arena, 0, s, k, v, L - 1)
+    q = W.normal((len(lens), dm), 190)
+    out = torch.full((len(lens), dm), float("nan"), device="cuda")
+    arena.decode_self(0, list(range(len(lens))), dev(q), out)
+    got = host(out)
+    for s, L in enumerate(lens):
+        k, v = data[s]
+        ref = attention_f64(q[s], k, v, 1, L, H, dm)
+        assert maxerr(got[s], ref.ravel()) <= TOL16, f"slot {s} L={L}"
+    arena.close()
+
+
 def test_self_decode_slot_order_and_subset(wrs, orc, ctx):
     # rows map to arbitrary slots; each slot has its own length
     from wrs_amd import workloads as W
@@ -191,10 +216,11 @@ def test_cross_decode_beam_counts(wrs, ctx, beams):
     arena.close()
 
 
-@pytest.mark.parametrize("n_audio", [129, 1536, 1537, 2900])
+@pytest.mark.parametrize("n_audio", [129, 200, 256, 257, 1536, 1537, 2900])
 def test_cross_decode_split_counts(wrs, ctx, n_audio):
-    # 128 keys per split: 2, 12 (largest one-round merge), 13 and 23 splits
-    # (batched merge) per (beam group, head).
+    # 129..256 keys: one 256-key workgroup per (beam group, head), two tiles per
+    # wave, no merge. Longer planes split into 128 keys: 3, 12 (largest one-round
+    # merge), 13 and 23 splits (batched merge).
     from wrs_amd import workloads as W
     H, dm, beams = 4, 256, 5
     note(f"device decode_cross n_audio={n_audio}")

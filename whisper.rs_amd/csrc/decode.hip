@@ -4,21 +4,22 @@
 //   (replaces crates/tensor/src/ops/attention.rs:246-434 single_token_mha_d64
 //    as called from crates/whisper/src/decoder.rs:636 / :698).
 //   Grid (split, head, group). A workgroup of 8 waves owns kChunk = 128
-//   consecutive keys (16 waves and 256 keys when that covers the whole
-//   sequence, so that no merge is needed) of one (group, head) plane and ALL
-//   query rows of the
+//   consecutive keys (256 when that covers the whole sequence, so that no
+//   merge is needed) of one (group, head) plane and ALL query rows of the
 //   group (the beams of an utterance share the cross-attention plane, so it is
-//   read once per step instead of once per beam). Each wave takes 16 keys,
-//   and every lane issues its q loads and its four 16-byte K/V loads before
-//   any arithmetic, so the whole layer's cache is in flight from the first
+//   read once per step instead of once per beam). Each wave takes one 16-key
+//   tile (two, 128 keys apart, in a 256-key workgroup: a 16-wave workgroup of
+//   one tile each cost ~1.2 us more per launch at any length), and every lane
+//   issues its q loads and its four 16-byte K/V loads per tile before any
+//   arithmetic, so the whole layer's cache is in flight from the first
 //   cycles. The arithmetic runs on the matrix pipe, in registers:
 //   - scores: one 16x16x32 f16 MFMA tile S^T = K Q^T per 32 d. The K rows
 //     are the A operand exactly as loaded (lane (c, g): key c, d 8g..8g+7).
 //     q*scale*log2(e) is scaled by a power of two per row and split into f16
 //     high and low parts, placed in B columns r and r+8; a row_ror-8 DPP adds
 //     the two columns, so the scores carry ~2^-22 relative error, not f16's.
-//   - softmax: the 16 keys' max and exp2 sum per row, over the lane's 4
-//     values and two cross-row moves.
+//   - softmax: the wave's keys' max and exp2 sum per row, over the lane's 4
+//     values per tile and two cross-row moves.
 //   - P V: V^T comes out of a 16x16x32 MFMA of the V rows against a 0/1
 //     selection matrix (exact), already in the B layout of a 16x16x16 MFMA
 //     whose A operand is P as produced by the score tile, again as high
@@ -128,13 +129,15 @@ __device__ inline float sum_x16_x32(float x) {
 }
 
 
-// kMWaves waves of one 16-key tile each: 8 (128 keys, kDecodeChunk) in
-// general, 16 (kDecodeChunkLong = 256 keys) when that covers the whole
-// sequence, which then needs no split-K merge.
-template <int R, int kMWaves>
+// kMWaves waves of kTiles 16-key tiles each: 8 waves of one tile (128 keys,
+// kDecodeChunk) in general, 8 waves of two (kDecodeChunkLong = 256 keys) when
+// that covers the whole sequence, which then needs no split-K merge. Tile t of
+// wave w covers keys 128t + 16w.. of the workgroup's chunk.
+template <int R, int kMWaves, int kTiles>
 __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   static_assert(kMWaves >= kMaxRowsPerGroup, "one merging wave per query row");
-  constexpr int kChunk = 16 * kMWaves;
+  static_assert(kMWaves == 8, "tile t of wave w starts at key 128t + 16w");
+  constexpr int kChunk = 16 * kMWaves * kTiles;
   __shared__ float red[kMWaves][16][kRedPitch];
   __shared__ float wm[kMWaves][8], wl[kMWaves][8];
   __shared__ int last_flag;
@@ -188,13 +191,15 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.k + plane), 0, range, kRawBuffer);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.v + plane), 0, range, kRawBuffer);
-  const uint32_t voff = static_cast<uint32_t>(kbase + col) * 128u + 16u * kg;
-  const u32x4 kx0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff, 0, 0));
-  const u32x4 kx1 =
-      __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff + 64, 0, 0));
-  const u32x4 vx0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, 0, 0));
-  const u32x4 vx1 =
-      __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 64, 0, 0));
+  u32x4 kx0[kTiles], kx1[kTiles], vx0[kTiles], vx1[kTiles];
+#pragma unroll
+  for (int tt = 0; tt < kTiles; ++tt) {
+    const uint32_t voff = static_cast<uint32_t>(kbase + 128 * tt + col) * 128u + 16u * kg;
+    kx0[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff, 0, 0));
+    kx1[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff + 64, 0, 0));
+    vx0[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, 0, 0));
+    vx1[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 64, 0, 0));
+  }
   // Every load above is issued before any of them is waited on: the q
   // arithmetic below depends on a value defined after them.
   float one;
@@ -257,27 +262,32 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
 
   // S^T tile: lane (col, kg) gets keys kbase+4kg+i of column col; the high and
   // low columns of a row are eight lanes apart (row_ror 8 adds them).
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kx0), b0, s, 0, 0, 0);
-  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kx1), b1, s, 0, 0, 0);
-  float sc[4], mx = -INFINITY;
+  float sc[kTiles][4], mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float si = s[i];
-    const float full = (si + dpp<0x128>(si)) * down;
-    sc[i] = (kbase + 4 * kg + i < len) ? full : -INFINITY;
-    mx = fmaxf(mx, sc[i]);
+  for (int tt = 0; tt < kTiles; ++tt) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kx0[tt]), b0, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kx1[tt]), b1, s, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float si = s[i];
+      const float full = (si + dpp<0x128>(si)) * down;
+      sc[tt][i] = (kbase + 128 * tt + 4 * kg + i < len) ? full : -INFINITY;
+      mx = fmaxf(mx, sc[tt][i]);
+    }
   }
   mx = max_x16_x32(mx);
   float sum = 0.f;
-  f16x4 pa;
+  f16x4 pa[kTiles];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float p = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc[i] - mx);
-    sum += p;
-    const _Float16 ph = static_cast<_Float16>(p);
-    pa[i] = lo_part ? static_cast<_Float16>(p - static_cast<float>(ph)) : ph;
-  }
+  for (int tt = 0; tt < kTiles; ++tt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc[tt][i] - mx);
+      sum += p;
+      const _Float16 ph = static_cast<_Float16>(p);
+      pa[tt][i] = lo_part ? static_cast<_Float16>(p - static_cast<float>(ph)) : ph;
+    }
   sum = sum_x16_x32(sum);
 
   // V^T by multiplying with a 0/1 selection matrix (exact), then P V.
@@ -290,10 +300,14 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-        __builtin_bit_cast(f16x8, dt < 2 ? vx0 : vx1), (dt & 1) ? e1 : e0, z, 0, 0, 0);
-    const f16x4 vb = __builtin_convertvector(t, f16x4);
-    const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, z, 0, 0, 0);
+    f32x4 o = z;
+#pragma unroll
+    for (int tt = 0; tt < kTiles; ++tt) {
+      const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          __builtin_bit_cast(f16x8, dt < 2 ? vx0[tt] : vx1[tt]), (dt & 1) ? e1 : e0, z, 0, 0, 0);
+      const f16x4 vb = __builtin_convertvector(t, f16x4);
+      o = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[tt], vb, o, 0, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][4 * kg + i][16 * dt + col] = o[i];
   }
@@ -504,13 +518,14 @@ size_t decode_counter_words(int n_groups, int n_heads) {
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s) {
   if (a.n_groups <= 0 || a.n_splits <= 0) return hipSuccess;
   if (a.chunk != kDecodeChunk && a.chunk != kDecodeChunkLong) return hipErrorInvalidValue;
+  static_assert(kDecodeChunk == 128 && kDecodeChunkLong == 256, "8 waves of one or two tiles");
   const bool lng = a.chunk == kDecodeChunkLong;
-  const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(lng ? 1024 : 512);
+  const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(512);
 #define WRS_DEC(R)                                                          \
   if (lng)                                                                  \
-    hipLaunchKernelGGL((decode_f16<R, 16>), grid, block, 0, s, a);          \
+    hipLaunchKernelGGL((decode_f16<R, 8, 2>), grid, block, 0, s, a);        \
   else                                                                      \
-    hipLaunchKernelGGL((decode_f16<R, 8>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((decode_f16<R, 8, 1>), grid, block, 0, s, a);
   switch (a.rows_per_group) {
     case 1: WRS_DEC(1) break;
     case 2: WRS_DEC(2) break;

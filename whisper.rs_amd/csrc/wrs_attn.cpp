@@ -313,7 +313,7 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
   a.n_groups = n_groups;
   a.rows_per_group = rows_per_group;
   a.n_heads = n_heads;
-  // Sequences of 129..256 keys take one 16-wave workgroup per (group, head):
+  // Sequences of 129..256 keys take one 256-key workgroup per (group, head):
   // no partials and no merge. Longer ones split into 128-key workgroups.
   a.chunk = (max_len > wrs::kDecodeChunk && max_len <= wrs::kDecodeChunkLong)
                 ? wrs::kDecodeChunkLong
