@@ -256,10 +256,28 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
         all_reads()
     ctx.use_torch_stream()
     floor_us = _replay_time_us(gf, reps, U * cfg.n_layers // 2)
+    # and what any launch costs in these replays: the same kernel over 16 bytes
+    # (one workgroup: one load, one store)
+    def all_tiny():
+        for base in bases:
+            for pair in range(cfg.n_layers // 2):
+                ctx.check(ctx._lib.wrs_stream_read(ctx.handle, base + pair * per, 16,
+                                                   sink.data_ptr(), sink.numel()),
+                          "wrs_stream_read")
+
+    all_tiny()
+    torch.cuda.synchronize()
+    gt = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gt):
+        ctx.use_torch_stream()
+        all_tiny()
+    ctx.use_torch_stream()
+    tiny_us = _replay_time_us(gt, reps, U * cfg.n_layers // 2)
     floor = {"bytes_per_launch": per, "us_per_launch": round(floor_us, 3),
-             "GBps": round(per / (floor_us * 1e-6) / 1e9, 1)}
+             "GBps": round(per / (floor_us * 1e-6) / 1e9, 1),
+             "one_workgroup_launch_us": round(tiny_us, 3)}
     log(f"decode: {us:.3f} us/launch ({gbs:.1f} GB/s); single-launch read floor "
-        f"{floor_us:.3f} us ({floor['GBps']} GB/s)")
+        f"{floor_us:.3f} us ({floor['GBps']} GB/s); one-workgroup launch {tiny_us:.3f} us")
     for ar in arenas:
         ar.close()
     return cfg, us, gbs, floor
