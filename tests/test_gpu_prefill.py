@@ -36,6 +36,16 @@ def schedule(request, monkeypatch):
     return request.param
 
 
+@pytest.fixture(params=[0, 1, 3], ids=["f32block", "f32ksplit", "f32ksplit3"])
+def f32_schedule(request, monkeypatch):
+    """The schedules of the f32 kernel on the same shapes: grids of up to four
+    128-query blocks per CU normally take the key-split workgroups (32 queries,
+    key tiles interleaved over four waves; three when forced to 3), larger ones
+    128-query blocks."""
+    monkeypatch.setenv("WRS_PREFILL_F32_SPLIT", str(request.param))
+    return request.param
+
+
 def _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal=False):
     out = np.zeros(t_q * d_model, np.float32)
     orc.flash_attention_2(np.ascontiguousarray(q.ravel()), np.ascontiguousarray(k.ravel()),
@@ -47,7 +57,7 @@ def _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal=False):
 # ---- host-slice drop-in: the reference's own known-answer tests -----------
 
 @pytest.mark.parametrize("t_q,t_kv,h,dh,causal", KAT_SHAPES)
-def test_host_slice_kat(wrs, orc, ctx, t_q, t_kv, h, dh, causal):
+def test_host_slice_kat(wrs, orc, ctx, t_q, t_kv, h, dh, causal, f32_schedule):
     note(f"host-slice flash_attention_2 t_q={t_q} t_kv={t_kv} h={h} dh={dh} causal={causal}")
     d_model, q, k, v = _kat_inputs(orc, t_q, t_kv, h, dh)
     out = np.full(t_q * d_model, np.nan, np.float32)
@@ -59,7 +69,7 @@ def test_host_slice_kat(wrs, orc, ctx, t_q, t_kv, h, dh, causal):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_host_slice_modular_inputs(wrs, orc, ctx, causal):
+def test_host_slice_modular_inputs(wrs, orc, ctx, causal, f32_schedule):
     # crates/tensor/tests/test_flash_attention.rs:3-98 (d_head 16, bound 1e-4)
     t_q, t_kv, n_heads, d_model = 64, 128, 4, 64
     note(f"host-slice modular inputs causal={causal}")
@@ -72,7 +82,7 @@ def test_host_slice_modular_inputs(wrs, orc, ctx, causal):
                   _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal)) <= TOL32
 
 
-def test_host_slice_causal_single_query_sees_first_key(wrs, orc, ctx):
+def test_host_slice_causal_single_query_sees_first_key(wrs, orc, ctx, f32_schedule):
     # test_flash_attention_tiled.rs:186-205
     note("host-slice causal single query")
     d_model, t_kv = 64, 17
@@ -83,7 +93,7 @@ def test_host_slice_causal_single_query_sees_first_key(wrs, orc, ctx):
     assert np.all(np.abs(out - v[:d_model]) <= 1e-6)
 
 
-def test_host_slice_overwrites_stale_output(wrs, orc, ctx):
+def test_host_slice_overwrites_stale_output(wrs, orc, ctx, f32_schedule):
     # test_flash_attention_tiled.rs:243-262
     note("host-slice stale NaN sentinel")
     t_q, t_kv, n_heads, d_model = 40, 100, 2, 128
@@ -129,7 +139,7 @@ def _encoder_run(wrs, ctx, cfg, q, k, v, dtype, batch=None):
     return host(out)
 
 
-def test_tiny_encoder_f32(wrs, orc, ctx):
+def test_tiny_encoder_f32(wrs, orc, ctx, f32_schedule):
     from wrs_amd import workloads as W
     cfg = W.TINY_ENCODER
     note(f"device prefill f32: {cfg.name}")
@@ -271,7 +281,7 @@ def test_prefill_causal_with_offset(wrs, ctx, t_q, t_kv, offset, schedule):
     assert maxerr(host(out), ref) <= TOL16
 
 
-def test_prefill_d_head_80_f16_inputs(wrs, ctx):
+def test_prefill_d_head_80_f16_inputs(wrs, ctx, f32_schedule):
     # d_head != 64 with 16-bit inputs runs the f32-MFMA kernel on widened values.
     from wrs_amd import workloads as W
     H, dh, t_q, t_kv = 2, 80, 37, 91

@@ -5,6 +5,10 @@
 // (prefill_f32_block.hpp holds the block routine and its semantics).
 #include "prefill_f32_block.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
 namespace wrs {
 namespace {
 
@@ -12,6 +16,7 @@ using f32blk::fa2_block;
 using f32blk::kM;
 using f32blk::kThreads;
 using f32blk::Tiles;
+using f32blk::f32x16;
 
 __device__ inline int xcd_remap(int pid, int nwg) {
   const int xcd = pid & 7, k = pid >> 3;
@@ -27,20 +32,257 @@ __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, in
   fa2_block<QT, KT, DB>(a, lid % n_qblk, bh % a.n_heads, bh / a.n_heads, tl);
 }
 
+// Small grids of 128-query blocks (whisper-tiny's encoder: 12 blocks x 6
+// heads = 72) leave most SIMDs idle, since one wave carries 32 queries through
+// every key. fa2_prefill_f32_ksplit runs one 32-query block per workgroup
+// instead, with S = 4 waves (2..4 when forced) that take the block's key tiles
+// in turn (tile t on wave t % S). Each wave keeps its own online softmax over
+// its tiles, in its own LDS tile pair, with the next tile's rows loading while
+// it computes. The workgroup then merges the S (max, sum, O) by the
+// log-sum-exp rule.
+constexpr int kQS = 32;       // queries per k-split workgroup
+constexpr int kMaxSplit = 4;  // waves per k-split workgroup, at most
+
+template <typename QT, typename KT, int DB>
+__global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f32_ksplit(
+    PrefillArgs a, int n_qblk, int vec) {
+  constexpr int D = 32 * DB;
+  constexpr int P = Tiles<DB>::P;
+  constexpr int kN = f32blk::kN;
+  constexpr int R = D + 1;  // merge row pitch: the 32 queries of one write hit distinct banks
+  __shared__ Tiles<DB> tl[kMaxSplit];
+  static_assert(sizeof(Tiles<DB>) >= (kQS * R + 2 * kQS) * sizeof(float), "merge rows fit");
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int qblk = lid % n_qblk;
+  const int bh = lid / n_qblk;
+  const int h = bh % a.n_heads, b = bh / a.n_heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int S = __builtin_amdgcn_readfirstlane(static_cast<int>(blockDim.x) >> 6);
+  const int r32 = lane & 31, hl = lane >> 5;
+  const int dh = a.d_head;
+  float* const Ks = tl[wave].k;
+  float* const Vs = tl[wave].v;
+
+  const QT* qp = static_cast<const QT*>(a.q) + b * a.lq.bs + h * a.lq.hs;
+  const KT* kp = static_cast<const KT*>(a.k) + b * a.lk.bs + h * a.lk.hs;
+  const KT* vp = static_cast<const KT*>(a.v) + b * a.lv.bs + h * a.lv.hs;
+
+  const int qi = qblk * kQS + r32;
+  const int qpos = qi + a.q_pos_offset;
+  float qf[D / 2];
+#pragma unroll
+  for (int kk = 0; kk < D / 2; ++kk) {
+    const int d = 2 * kk + hl;
+    qf[kk] = (qi < a.t_q && d < dh) ? f32blk::widen(qp[static_cast<int64_t>(qi) * a.lq.rs + d]) : 0.f;
+  }
+  int kv_end = a.t_kv;
+  if (a.causal) {
+    const int last = min(qblk * kQS + kQS, a.t_q) - 1 + a.q_pos_offset;
+    kv_end = min(kv_end, last + 1);
+  }
+
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = f32x16{};
+  float m = -INFINITY, l = 0.f;
+
+  auto wave_sync = [] {
+    // LDS operations of one wave complete in order: this orders the wave's
+    // tile reads before its next writes, and its writes before its reads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // The same per-tile arithmetic as fa2_block (attention.rs:141-222).
+  auto tile = [&](int j0) {
+    // Four independent accumulator chains over d: with one wave per SIMD a
+    // single chain would wait out every MFMA's latency.
+    f32x16 sp[4] = {};
+#pragma unroll
+    for (int kk = 0; kk < D / 2; ++kk)
+      sp[kk & 3] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk],
+                                                         sp[kk & 3], 0, 0, 0);
+    f32x16 sc = (sp[0] + sp[1]) + (sp[2] + sp[3]);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = j0 + 8 * (i >> 2) + 4 * hl + (i & 3);
+      float x = a.scale * sc[i];
+      if (key >= a.t_kv || (a.causal && key > qpos)) x = -INFINITY;
+      sc[i] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    m = m_new;
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sc[i] = expf(sc[i] - m_use);
+      ls += sc[i];
+    }
+    l = l * alpha + ls;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int key = 8 * (t >> 2) + 4 * hl + (t & 3);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * P + db * 32 + r32], sc[t], o[db],
+                                                     0, 0, 0);
+    }
+  };
+
+  if constexpr (std::is_same<KT, float>::value) {
+    if (vec) {
+      // f32 K/V rows of exactly D floats, 16-byte aligned: lane (key, half)
+      // loads half a K row and half a V row as float4s, one tile ahead of the
+      // tile it computes.
+      const int key = lane >> 1, c0 = (lane & 1) * (D / 2);
+      f32x4 kr[D / 8], vr[D / 8];
+      auto load = [&](int j0) {
+        const bool ok = j0 + key < a.t_kv;
+        const float* krow = kp + static_cast<int64_t>(j0 + key) * a.lk.rs + c0;
+        const float* vrow = vp + static_cast<int64_t>(j0 + key) * a.lv.rs + c0;
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+          kr[i] = ok ? *reinterpret_cast<const f32x4*>(krow + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+          vr[i] = ok ? *reinterpret_cast<const f32x4*>(vrow + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      };
+      int j0 = wave * kN;
+      if (j0 < kv_end) load(j0);
+      for (; j0 < kv_end; j0 += S * kN) {
+        wave_sync();
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            Ks[key * P + c0 + 4 * i + c] = kr[i][c];
+            Vs[key * P + c0 + 4 * i + c] = vr[i][c];
+          }
+        wave_sync();
+        if (j0 + S * kN < kv_end) load(j0 + S * kN);
+        tile(j0);
+      }
+    }
+  }
+  if (!(std::is_same<KT, float>::value && vec)) {
+    for (int j0 = wave * kN; j0 < kv_end; j0 += S * kN) {
+      wave_sync();
+#pragma unroll 4
+      for (int e = lane; e < kN * D; e += 64) {
+        const int key = e / D, d = e % D;
+        float kv = 0.f, vv = 0.f;
+        if (j0 + key < a.t_kv && d < dh) {
+          kv = f32blk::widen(kp[static_cast<int64_t>(j0 + key) * a.lk.rs + d]);
+          vv = f32blk::widen(vp[static_cast<int64_t>(j0 + key) * a.lv.rs + d]);
+        }
+        Ks[key * P + d] = kv;
+        Vs[key * P + d] = vv;
+      }
+      wave_sync();
+      tile(j0);
+    }
+  }
+  l += __shfl_xor(l, 32);
+
+  // Merge rows in the wave's own tile pair (both tiles, as one array): O
+  // [32][R] (query-major), then m and l per query.
+  __syncthreads();  // every wave is past its last tile reads
+  float* const mo = reinterpret_cast<float*>(&tl[wave]);
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+      mo[r32 * R + d] = o[db][i];
+    }
+  if (hl == 0) {
+    mo[kQS * R + r32] = m;
+    mo[kQS * R + kQS + r32] = l;
+  }
+  __syncthreads();
+  // Thread t merges element e = t, t + 64S, ... of the block's 32 x dh outputs.
+  for (int e = tid; e < kQS * dh; e += 64 * S) {
+    const int mq = e / dh, d = e % dh;
+    const int oq = qblk * kQS + mq;
+    if (oq >= a.t_q) continue;
+    float M = -INFINITY;
+    for (int w = 0; w < S; ++w) M = fmaxf(M, reinterpret_cast<const float*>(&tl[w])[kQS * R + mq]);
+    float L = 0.f, acc = 0.f;
+    for (int w = 0; w < S; ++w) {
+      const float* t = reinterpret_cast<const float*>(&tl[w]);
+      const float mw = t[kQS * R + mq];
+      const float ew = (mw == -INFINITY) ? 0.f : expf(mw - M);
+      L += ew * t[kQS * R + kQS + mq];
+      acc += ew * t[mq * R + d];
+    }
+    a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] =
+        acc * ((L > 0.f) ? 1.f / L : 0.f);
+  }
+}
+
+// CUs of the current device, read once.
+int device_cus() {
+  static const int cus = [] {
+    int dev = 0, n = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+      (void)hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    return n;
+  }();
+  return cus;
+}
+
 template <typename QT, typename KT>
 hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   const int n_qblk = (a.t_q + kM - 1) / kM;
-  const int64_t nwg = static_cast<int64_t>(n_qblk) * a.n_heads * a.batch;
+  const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
+  const int64_t nwg = n_qblk * bh;
   if (nwg <= 0) return hipSuccess;
+  const int db = (a.d_head + 31) / 32;
+  if (db < 1 || db > 4) return hipErrorInvalidValue;
+  // WRS_PREFILL_F32_SPLIT=0 forces 128-query blocks, 1 the key split, 2..4 the
+  // key split over that many waves (tests, measurements).
+  const char* force = std::getenv("WRS_PREFILL_F32_SPLIT");
+  const int forced = force ? std::atoi(force) : -1;
+  // The key split, four waves per 32-query block, up to 4 blocks of 128
+  // queries per CU; beyond that the 128-query blocks, whose four waves share
+  // every tile load, have waves enough. Measured (f32, d_head 64, one window):
+  // 1500 x 6 heads 94 against 208 us, 4096 x 6 heads 341 against 711 us,
+  // 1500 x 32 heads 279 against 347 us, 1500 x 320 heads 2447 against 2150 us.
+  const int n_qs = (a.t_q + kQS - 1) / kQS;
+  const int64_t nws = n_qs * bh;
+  const int split = forced >= 2 ? std::min(forced, kMaxSplit) : kMaxSplit;
+  if (forced >= 1 || (forced != 0 && nwg <= 4 * static_cast<int64_t>(device_cus()))) {
+    if (nws > 0x7fffffff) return hipErrorInvalidConfiguration;
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const int vec = a.d_head == 32 * db && a.lk.rs % 4 == 0 && a.lv.rs % 4 == 0 &&
+                    a.lk.bs % 4 == 0 && a.lv.bs % 4 == 0 && a.lk.hs % 4 == 0 &&
+                    a.lv.hs % 4 == 0 && al16(a.k) && al16(a.v);
+    const dim3 grid(static_cast<unsigned>(nws)), block(64 * split);
+    switch (db) {
+      case 1: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 1>), grid, block, 0, s, a, n_qs, vec); break;
+      case 2: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 2>), grid, block, 0, s, a, n_qs, vec); break;
+      case 3: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 3>), grid, block, 0, s, a, n_qs, vec); break;
+      default: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 4>), grid, block, 0, s, a, n_qs, vec); break;
+    }
+    return hipGetLastError();
+  }
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads);
-  const int db = (a.d_head + 31) / 32;
   switch (db) {
     case 1: hipLaunchKernelGGL((fa2_prefill_f32<QT, KT, 1>), grid, block, 0, s, a, n_qblk); break;
     case 2: hipLaunchKernelGGL((fa2_prefill_f32<QT, KT, 2>), grid, block, 0, s, a, n_qblk); break;
     case 3: hipLaunchKernelGGL((fa2_prefill_f32<QT, KT, 3>), grid, block, 0, s, a, n_qblk); break;
-    case 4: hipLaunchKernelGGL((fa2_prefill_f32<QT, KT, 4>), grid, block, 0, s, a, n_qblk); break;
-    default: return hipErrorInvalidValue;
+    default: hipLaunchKernelGGL((fa2_prefill_f32<QT, KT, 4>), grid, block, 0, s, a, n_qblk); break;
   }
   return hipGetLastError();
 }
