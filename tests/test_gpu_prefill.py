@@ -68,6 +68,23 @@ def test_host_slice_kat(wrs, orc, ctx, t_q, t_kv, h, dh, causal, f32_schedule):
     assert maxerr(out.reshape(t_q, d_model), ref) <= TOL32
 
 
+@pytest.mark.parametrize("dh,causal", [(32, False), (96, True), (128, False), (128, True)])
+def test_host_slice_head_sizes(wrs, orc, ctx, dh, causal, f32_schedule):
+    # d_head 32, 96 and 128: one, three and four 32-wide d blocks, rows of exactly
+    # that many floats (the key split's float4 row loads)
+    t_q, t_kv, h = 70, 133, 3
+    d_model = h * dh
+    note(f"host-slice flash_attention_2 d_head={dh} causal={causal}")
+    rng = orc.Rng(0x5EED ^ dh)
+    q, k, v = rng.fill(t_q * d_model), rng.fill(t_kv * d_model), rng.fill(t_kv * d_model)
+    out = np.full(t_q * d_model, np.nan, np.float32)
+    wrs.flash_attention_2(q, k, v, t_q, t_kv, h, d_model, causal, out, ctx=ctx)
+    ref = attention_f64(q, k, v, t_q, t_kv, h, d_model, causal)
+    assert maxerr(out.reshape(t_q, d_model), ref) <= TOL32
+    assert maxerr(out.reshape(t_q, d_model),
+                  _oracle_fa2(orc, q, k, v, t_q, t_kv, h, d_model, causal)) <= TOL32
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_host_slice_modular_inputs(wrs, orc, ctx, causal, f32_schedule):
     # crates/tensor/tests/test_flash_attention.rs:3-98 (d_head 16, bound 1e-4)
