@@ -3,8 +3,11 @@
 //  called per text layer from decoder.rs:709-721 for DTW word timestamps).
 //
 // K5 (capture_cross_f16<pass>): one workgroup per (query block, key chunk,
-//   pair), ordered so that the query blocks of one key chunk run on one XCD and
-//   share its L2. Two launches of the same kernel, or one when the attention
+//   pair), placed so that every query block of a key chunk runs on the XCD
+//   that chunk belongs to, and the chunk's K rows are fetched into one L2
+//   only. A call small enough for four XCDs (at most 128 workgroups, one per
+//   CU) uses four, so that the query rows, which every XCD in use reads, are
+//   fetched four times instead of eight. Two launches of the same kernel, or one when the attention
 //   pass over the same q and keys left its row statistics (pass 2 below). A
 //   workgroup of 4 waves owns 16 query rows of
 //   one (slot, head) pair and one chunk of 128 keys of that head's f16 cross
@@ -59,29 +62,28 @@ __device__ inline f32x4 mfma16(const u32x4& a, const f16x8& b, const f32x4& c) {
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
 __device__ inline int clamp_exp(int e) { return e < -126 ? -126 : (e > 127 ? 127 : e); }
 
-// Workgroup p of a launch runs on XCD p mod 8; consecutive work items should
-// share an XCD, so item = the p-th of that XCD's share.
-__device__ inline int xcd_remap(int pid, int nwg) {
-  const int xcd = pid & 7, k = pid >> 3;
-  const int per = nwg >> 3, rem = nwg & 7;
-  return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
-}
+// Workgroup p of a launch runs on XCD p mod 8 (the dispatcher's round robin).
+// Of n_xcd XCDs in use, XCD x takes chunks x, x + n_xcd, ...: the grid holds
+// 8 * ceil(n_chunks / n_xcd) chunk slots per (pair, block), and workgroups on
+// an XCD not in use, or of a slot past the last chunk, return at once. The
+// placement decides only which L2 fetches what.
+constexpr int kXcds = 8;
 
 template <int kPass>
 __global__ __launch_bounds__(kThreads) void capture_cross_f16(CaptureArgs a, int n_blocks,
-                                                               int n_chunks) {
+                                                               int n_chunks, int n_xcd) {
+  const int n_slots = (n_chunks + n_xcd - 1) / n_xcd;  // chunk slots per XCD
+  const int xcd = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
+  const int block = k % n_blocks;
+  const int chunk = xcd + n_xcd * ((k / n_blocks) % n_slots);
+  const int pair = k / (n_blocks * n_slots);
+  if (xcd >= n_xcd || chunk >= n_chunks) return;
   __shared__ float red[kWaves][kRows];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15;  // query column of this lane (B operand, C column)
   const int g = lane >> 4;  // k-group of the operands; keys 4g..4g+3 of a C tile
-  // Work item = block + n_blocks * (chunk + n_chunks * pair): the query blocks
-  // of one chunk are consecutive items, hence on one XCD.
-  const int item = xcd_remap(blockIdx.x, gridDim.x);
-  const int block = item % n_blocks;
-  const int chunk = (item / n_blocks) % n_chunks;
-  const int pair = item / (n_blocks * n_chunks);
   const int head = a.head[pair];
   const int row = block * kRows + n;
   const bool row_ok = row < a.n_tokens;
@@ -258,17 +260,20 @@ hipError_t launch_capture_cross_f16(const CaptureArgs& a, hipStream_t s) {
   if (a.n_tokens <= 0 || a.n_pairs <= 0 || a.n_audio <= 0) return hipSuccess;
   const int n_chunks = (a.n_audio + kChunkKeys - 1) / kChunkKeys;
   const int n_blocks = (a.n_tokens + kRows - 1) / kRows;
-  const int64_t items = static_cast<int64_t>(n_chunks) * n_blocks * a.n_pairs;
+  const int64_t work = static_cast<int64_t>(n_chunks) * n_blocks * a.n_pairs;
+  const int n_xcd = work <= 128 ? 4 : kXcds;
+  const int64_t items =
+      static_cast<int64_t>(kXcds) * ((n_chunks + n_xcd - 1) / n_xcd) * n_blocks * a.n_pairs;
   if (items > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(items));
   if (a.lse) {
-    hipLaunchKernelGGL(capture_cross_f16<2>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks);
+    hipLaunchKernelGGL(capture_cross_f16<2>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks, n_xcd);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(capture_cross_f16<0>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks);
+  hipLaunchKernelGGL(capture_cross_f16<0>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks, n_xcd);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(capture_cross_f16<1>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks);
+  hipLaunchKernelGGL(capture_cross_f16<1>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks, n_xcd);
   return hipGetLastError();
 }
 
