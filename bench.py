@@ -969,7 +969,8 @@ def main():
     ap.add_argument("--stream-reps", type=int, default=20)
     ap.add_argument("--rows-reps", type=int, default=50)
     ap.add_argument("--only", choices=["encoder", "encoder_base", "decode", "decode_self",
-                                       "capture", "linear", "stream", "rows", "traffic"],
+                                       "capture", "linear", "stream", "rows", "host_slice",
+                                       "traffic"],
                     default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
@@ -1022,6 +1023,12 @@ def main():
         calibration_copy()
         log(f"stream only: step {sms:.3f} ms, {sgbs:.1f} GB/s; vocabulary {vms * 1e3:.1f} us, "
             f"{vgbs:.1f} GB/s")
+        return
+    if args.only == "host_slice":
+        hs = bench_host_slice(wrs, W, ctx, reps=100)
+        log(f"host_slice only: host slices {hs['host_slice_ms']:.3f} ms/call, "
+            f"device-resident {hs['device_resident_ms'] * 1e3:.1f} us/call "
+            f"({hs['device_resident_value'] / 1e3:.1f} TFLOP/s)")
         return
     if args.only == "capture":
         _, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps, use_graph=not args.eager)
