@@ -63,6 +63,15 @@ void wrs_attn_destroy(wrs_attn_ctx *ctx);
 int wrs_attn_set_stream(wrs_attn_ctx *ctx, void *hip_stream);
 void *wrs_attn_get_stream(wrs_attn_ctx *ctx);
 int wrs_attn_synchronize(wrs_attn_ctx *ctx);
+/* Work decomposition of this context's prefill calls (wrs_attn_prefill, the
+ * host-slice drop-ins and the prompt-row entry points); results do not depend
+ * on it beyond floating-point summation order. No reference counterpart: the
+ * reference's tiling is fixed (Q_TILE = KV_TILE = 128, attention.rs:13,26).
+ * prefill_queries: queries per workgroup of the f16/bf16 kernel, 128 or 256,
+ * or 0 to choose by grid size (the default). f32_split: -1 chooses by
+ * grid size (the default), 0 runs 128-query blocks, 1 the four-wave key
+ * split, 2..4 the key split over that many waves. Other values: WRS_EINVAL. */
+int wrs_attn_set_schedule(wrs_attn_ctx *ctx, int prefill_queries, int f32_split);
 /* Text of the last error on this context (valid until the next call). */
 const char *wrs_attn_last_error(wrs_attn_ctx *ctx);
 const char *wrs_attn_status_string(int status);

@@ -85,6 +85,11 @@ pub mod ffi {
         pub fn wrs_attn_destroy(ctx: *mut WrsCtx);
         pub fn wrs_attn_set_stream(ctx: *mut WrsCtx, hip_stream: *mut c_void) -> c_int;
         pub fn wrs_attn_get_stream(ctx: *mut WrsCtx) -> *mut c_void;
+        pub fn wrs_attn_set_schedule(
+            ctx: *mut WrsCtx,
+            prefill_queries: c_int,
+            f32_split: c_int,
+        ) -> c_int;
         pub fn wrs_attn_synchronize(ctx: *mut WrsCtx) -> c_int;
         pub fn wrs_attn_last_error(ctx: *mut WrsCtx) -> *const c_char;
         pub fn wrs_attn_status_string(status: c_int) -> *const c_char;

@@ -36,7 +36,11 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def wrs():
-    return load_wrs_amd()
+    mod = load_wrs_amd()
+    # Name the library build this session calls (the in-tree one unless
+    # WRS_ATTN_LIB points elsewhere).
+    print(f"\n[wrs_amd] library: {mod._lib.LIB_PATH}", flush=True)
+    return mod
 
 
 @pytest.fixture(scope="session")

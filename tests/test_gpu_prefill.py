@@ -29,21 +29,23 @@ def ctx(wrs):
 
 
 @pytest.fixture(params=[128, 256], ids=["wg128", "wg256"])
-def schedule(request, monkeypatch):
+def schedule(request, ctx):
     """Both workgroup sizes of the 16-bit kernel on the same shapes: small grids
     normally take 128-query workgroups, large ones 256."""
-    monkeypatch.setenv("WRS_PREFILL_QUERIES", str(request.param))
-    return request.param
+    ctx.set_schedule(prefill_queries=request.param)
+    yield request.param
+    ctx.set_schedule()
 
 
 @pytest.fixture(params=[0, 1, 3], ids=["f32block", "f32ksplit", "f32ksplit3"])
-def f32_schedule(request, monkeypatch):
+def f32_schedule(request, ctx):
     """The schedules of the f32 kernel on the same shapes: grids of up to four
     128-query blocks per CU normally take the key-split workgroups (32 queries,
     key tiles interleaved over four waves; three when forced to 3), larger ones
     128-query blocks."""
-    monkeypatch.setenv("WRS_PREFILL_F32_SPLIT", str(request.param))
-    return request.param
+    ctx.set_schedule(f32_split=request.param)
+    yield request.param
+    ctx.set_schedule()
 
 
 def _oracle_fa2(orc, q, k, v, t_q, t_kv, n_heads, d_model, causal=False):

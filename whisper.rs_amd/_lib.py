@@ -11,9 +11,11 @@ import re
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
-# WRS_ATTN_LIB selects another build of the library (same C ABI); by default
-# the one built in the package's lib/ directory.
-LIB_PATH = Path(os.environ.get("WRS_ATTN_LIB") or PKG_DIR / "lib" / "libwrs_attn.so")
+# WRS_ATTN_LIB selects another build of the library (same C ABI) for A/B
+# measurements; by default the one built in the package's lib/ directory.
+# Loading another build is announced on stderr.
+DEFAULT_LIB_PATH = PKG_DIR / "lib" / "libwrs_attn.so"
+LIB_PATH = Path(os.environ.get("WRS_ATTN_LIB") or DEFAULT_LIB_PATH)
 HEADER_PATH = PKG_DIR.parent / "include" / "wrs_attn.h"
 
 WRS_OK = 0
@@ -55,6 +57,7 @@ _SIGNATURES = {
     "wrs_attn_destroy": (None, [_vp]),
     "wrs_attn_set_stream": (_int, [_vp, _vp]),
     "wrs_attn_get_stream": (_vp, [_vp]),
+    "wrs_attn_set_schedule": (_int, [_vp, _int, _int]),
     "wrs_attn_synchronize": (_int, [_vp]),
     "wrs_attn_last_error": (ctypes.c_char_p, [_vp]),
     "wrs_attn_status_string": (ctypes.c_char_p, [_int]),
@@ -131,8 +134,18 @@ def lib() -> ctypes.CDLL:
         if not LIB_PATH.exists():
             raise ExtensionMissing(
                 f"HIP extension not built: {LIB_PATH} is missing (run __graft_entry__.build())")
+        if LIB_PATH.resolve() != DEFAULT_LIB_PATH.resolve():
+            import sys
+            print(f"[wrs_amd] WRS_ATTN_LIB: loading {LIB_PATH}, not {DEFAULT_LIB_PATH}",
+                  file=sys.stderr, flush=True)
         L = ctypes.CDLL(str(LIB_PATH))
+        other = LIB_PATH.resolve() != DEFAULT_LIB_PATH.resolve()
         for name, (res, args) in _SIGNATURES.items():
+            if other and not hasattr(L, name):
+                # another build for an A/B measurement may predate an entry point
+                import sys
+                print(f"[wrs_amd] {LIB_PATH} lacks {name}", file=sys.stderr, flush=True)
+                continue
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args

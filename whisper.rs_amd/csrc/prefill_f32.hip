@@ -249,10 +249,9 @@ hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   if (nwg <= 0) return hipSuccess;
   const int db = (a.d_head + 31) / 32;
   if (db < 1 || db > 4) return hipErrorInvalidValue;
-  // WRS_PREFILL_F32_SPLIT=0 forces 128-query blocks, 1 the key split, 2..4 the
-  // key split over that many waves (tests, measurements).
-  const char* force = std::getenv("WRS_PREFILL_F32_SPLIT");
-  const int forced = force ? std::atoi(force) : -1;
+  // a.force_f32_split: 0 forces 128-query blocks, 1 the key split, 2..4 the
+  // key split over that many waves.
+  const int forced = a.force_f32_split;
   // The key split, four waves per 32-query block, up to 4 blocks of 128
   // queries per CU; beyond that the 128-query blocks, whose four waves share
   // every tile load, have waves enough. Measured (f32, d_head 64, one window):

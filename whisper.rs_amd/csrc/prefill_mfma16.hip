@@ -49,7 +49,6 @@
 #include "prefill_f32_block.hpp"
 #include "wrs_internal.hpp"
 
-#include <cstdlib>
 #include <type_traits>
 
 namespace wrs {
@@ -72,7 +71,9 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kN = 64;              // keys per tile
 constexpr int kNB = 4;              // LDS tile buffers
 constexpr int kTileH = kN * 64;     // 16-bit elements per K (or V) tile: 8 KiB
-constexpr int kRowsPerWave = kN / kWaves;
+constexpr int kRowsPerWave = kN / kWaves;  // tile rows one wave copies
+constexpr int kRowGroups = kRowsPerWave / 8;  // one 1 KiB DMA per 8 rows
+constexpr int kDmaPerTile = 2 * kRowGroups;   // K and V
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSumLimit = 16384.0f;  // row sum of one step that forces a rescale
 constexpr float kNoMax = -1.0e30f;     // reference max before the first step
@@ -127,6 +128,15 @@ __device__ inline u32x2 read_tr(const uint16_t* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_s16x4*)(reinterpret_cast<uintptr_t>(p)));
   return __builtin_bit_cast(u32x2, v);
+}
+
+// The same from an LDS byte address, and 16 bytes at one.
+__device__ inline u32x2 read_tr_at(uint32_t addr) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)addr);
+  return __builtin_bit_cast(u32x2, v);
+}
+__device__ inline u32x4 lds_read16(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)addr;
 }
 
 // 16-byte chunk swizzle of a 128-byte tile row: chunk c of row r is stored at
@@ -185,8 +195,7 @@ __device__ inline void tile_barrier() {
 template <int N>
 __device__ inline void wait_tiles() {
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -197,14 +206,48 @@ constexpr int queries_per_wg() {
   return 32 * QB * kWaves;
 }
 
+// Software pipeline of a full 32-key step (see full_step in the kernel): one
+// big MFMA per slot, 8*QB slots; unit u (two scores of block u/8, one packed
+// f16 register) has its FMAs in slot pipe_fma_slot(u), exp2 in the next slot
+// and the pack in the one after; block jb's row sums follow its last pack.
+template <int QB>
+constexpr int kSlots() {
+  return 8 * QB;
+}
+#ifndef WRS_PIPE_A
+#define WRS_PIPE_A 2
+#define WRS_PIPE_B 3
+#endif
+#ifndef WRS_QK_SEQ
+#define WRS_QK_SEQ 0
+#endif
+constexpr int pipe_fma_slot(int u) { return (WRS_PIPE_A * u) / WRS_PIPE_B; }
+constexpr int pipe_rowsum_slot(int jb) { return pipe_fma_slot(8 * jb + 7) + 3; }
+// Program order must respect the data flow: the pack of unit u overwrites
+// register pb[u/8][(u/4)%2] after the P V MFMAs of the previous step have read
+// it (slots 4*jb + 2*k2 + {0, 1}), and every pack and row sum falls inside the
+// step.
+template <int QB>
+constexpr bool pipe_order_ok() {
+  for (int u = 0; u < 8 * QB; ++u) {
+    const int jb = u >> 3, k2 = (u >> 2) & 1;
+    if (pipe_fma_slot(u) + 2 < 4 * jb + 2 * k2 + 1) return false;
+    if (pipe_fma_slot(u) + 2 >= kSlots<QB>()) return false;
+  }
+  for (int jb = 0; jb < QB; ++jb)
+    if (pipe_rowsum_slot(jb) >= kSlots<QB>()) return false;
+  return true;
+}
+static_assert(pipe_order_ok<1>() && pipe_order_ok<2>(), "pipelined step order");
+
 template <typename T, int QB>
 __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, int n_qblk) {
   constexpr int kQB = QB;
   constexpr int kM = queries_per_wg<QB>();
   typedef f32x16 SBlk[kQB];
   typedef u32x4 PBlk[kQB][2];
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kNB * kTileH];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kNB * kTileH];
+  __shared__ __attribute__((aligned(128))) uint16_t Ks[kNB * kTileH];
+  __shared__ __attribute__((aligned(128))) uint16_t Vs[kNB * kTileH];
   __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
   static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Ks), "f32 tiles fit in the K buffers");
   static_assert(kThreads == f32blk::kThreads && kM % f32blk::kM == 0, "whole f32 blocks");
@@ -254,15 +297,16 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   int first_masked = a.t_kv / 32;
   if (a.causal) first_masked = min(first_masked, (qblk * kM + a.q_pos_offset + 1) / 32);
 
-  // Tile copy: wave w moves rows 16w..16w+15 of each K and V tile, 8 rows
-  // (1 KiB, one DMA) at a time; lane i carries row i/8, chunk i%8 of them.
-  const int crow0 = kRowsPerWave * wave + (lane >> 3);
-  const int crow1 = crow0 + 8;
-  const int cch0 = (lane & 7) ^ swz(crow0), cch1 = (lane & 7) ^ swz(crow1);
-  const uint32_t kofs0 = static_cast<uint32_t>((crow0 * a.lk.rs + cch0 * 8) * 2);
-  const uint32_t kofs1 = static_cast<uint32_t>((crow1 * a.lk.rs + cch1 * 8) * 2);
-  const uint32_t vofs0 = static_cast<uint32_t>((crow0 * a.lv.rs + cch0 * 8) * 2);
-  const uint32_t vofs1 = static_cast<uint32_t>((crow1 * a.lv.rs + cch1 * 8) * 2);
+  // Tile copy: wave w moves rows kRowsPerWave*w.. of each K and V tile, 8
+  // rows (1 KiB, one DMA) at a time; lane i carries row i/8, chunk i%8 of them.
+  uint32_t kofs[kRowGroups], vofs[kRowGroups];
+#pragma unroll
+  for (int r = 0; r < kRowGroups; ++r) {
+    const int crow = kRowsPerWave * wave + 8 * r + (lane >> 3);
+    const int cch = (lane & 7) ^ swz(crow);
+    kofs[r] = static_cast<uint32_t>((crow * a.lk.rs + cch * 8) * 2);
+    vofs[r] = static_cast<uint32_t>((crow * a.lv.rs + cch * 8) * 2);
+  }
   const uint32_t kstep = static_cast<uint32_t>(kN * a.lk.rs * 2);
   const uint32_t vstep = static_cast<uint32_t>(kN * a.lv.rs * 2);
   const u32x4 krs = buffer_rsrc(kp, static_cast<uint32_t>(((a.t_kv - 1) * a.lk.rs + 64) * 2));
@@ -271,16 +315,16 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const uint32_t vs_lds = lds_addr(Vs) + wave * kRowsPerWave * 128;
   auto issue_tile = [&](int t) {
     const uint32_t buf = __builtin_amdgcn_readfirstlane((t % kNB) * (kTileH * 2));
-    dma16(krs, ks_lds + buf, kofs0 + t * kstep);
-    dma16(krs, ks_lds + buf + 1024, kofs1 + t * kstep);
-    dma16(vrs, vs_lds + buf, vofs0 + t * vstep);
-    dma16(vrs, vs_lds + buf + 1024, vofs1 + t * vstep);
+#pragma unroll
+    for (int r = 0; r < kRowGroups; ++r) dma16(krs, ks_lds + buf + 1024 * r, kofs[r] + t * kstep);
+#pragma unroll
+    for (int r = 0; r < kRowGroups; ++r) dma16(vrs, vs_lds + buf + 1024 * r, vofs[r] + t * vstep);
   };
   // bf16 V -> f16 in place: this wave's own rows, whose loads have landed.
   auto convert_tile = [&](int t) {
     if constexpr (Elem<T>::kConvertV) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < kRowGroups; ++r) {
         u32x4* p = reinterpret_cast<u32x4*>(Vs + (t % kNB) * kTileH + wave * kRowsPerWave * 64 +
                                             r * 512 + lane * 8);
         *p = Elem<T>::to_f16(*p);
@@ -288,39 +332,38 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     }
   };
 
-  // Per-lane LDS offsets (elements) of the MFMA operand reads. K A operand:
-  // row r32, chunks hl + 2*dk. V^T operand (transposed read): lane group
-  // g = lane/16 reads rows 4*(g/2) + (lane%16)/4 [+8] at columns
-  // 16*(g%2) + 4*(lane%4) [+32], so lane (d, hl) receives keys 4*hl + 0..3 [+8].
-  int koff[4];
-#pragma unroll
-  for (int dk = 0; dk < 4; ++dk) koff[dk] = r32 * 64 + (((hl + 2 * dk) ^ swz(r32)) * 8);
+  // Per-lane LDS byte offsets of the MFMA operand reads, as one base per
+  // operand and XOR masks. K A operand: row r32, 16-byte chunk
+  // (hl + 2*dk) ^ swz(r32) = (hl ^ swz(r32)) ^ 2*dk, i.e. the base XOR 32*dk.
+  // V^T operand (transposed read): lane group g = lane/16 reads rows
+  // r0 = 4*(g/2) + (lane%16)/4 [+8*e] at columns 16*(g%2) + 4*(lane%4)
+  // [+32*cc], so lane (d, hl) receives keys 4*hl + 0..3 [+8]. Row r0 + 8 has
+  // swz(r0) ^ 2, and chunk c0 + 4 = c0 ^ 4, so operand (e, cc) sits at the
+  // base + 1024*e, XOR 64*cc + 32*e. The masks touch bits 5-6 only and the
+  // tile buffers are 128-byte aligned, so they apply to whole LDS addresses.
+  const uint32_t koff0 = static_cast<uint32_t>(r32 * 128 + ((hl ^ swz(r32)) * 16));
   const int g = lane >> 4, t4 = lane & 15;
-  int voff[2][2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int row = 4 * (g >> 1) + (t4 >> 2) + 8 * e;
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const int chunk = 2 * (g & 1) + ((t4 & 3) >> 1) + 4 * cc;
-      voff[e][cc] = row * 64 + ((chunk ^ swz(row)) * 8) + 4 * (t4 & 1);
-    }
-  }
+  const int vr0 = 4 * (g >> 1) + (t4 >> 2), vc0 = 2 * (g & 1) + ((t4 & 3) >> 1);
+  const uint32_t voff0 = static_cast<uint32_t>(vr0 * 128 + ((vc0 ^ swz(vr0)) * 16) + 8 * (t4 & 1));
+  auto k_base = [&](int step) {
+    return lds_addr(Ks) + ((step >> 1) % kNB) * (kTileH * 2) + (step & 1) * 32 * 128 + koff0;
+  };
   auto kfetch = [&](int step, u32x4 (&ka)[4]) {
-    const uint16_t* kt = Ks + ((step >> 1) % kNB) * kTileH + (step & 1) * 32 * 64;
+    const uint32_t kb = k_base(step);
 #pragma unroll
-    for (int dk = 0; dk < 4; ++dk) ka[dk] = *reinterpret_cast<const u32x4*>(kt + koff[dk]);
+    for (int dk = 0; dk < 4; ++dk) ka[dk] = lds_read16(kb ^ (32u * dk));
   };
   auto vfetch = [&](int step, u32x2 (&va)[8]) {
-    const uint16_t* vt = Vs + ((step >> 1) % kNB) * kTileH + (step & 1) * 32 * 64;
+    const uint32_t vb =
+        lds_addr(Vs) + ((step >> 1) % kNB) * (kTileH * 2) + (step & 1) * 32 * 128 + voff0;
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      const uint16_t* v0 = vt + 16 * k2 * 64;
-      va[4 * k2 + 0] = read_tr(v0 + voff[0][0]);
-      va[4 * k2 + 1] = read_tr(v0 + voff[1][0]);
-      va[4 * k2 + 2] = read_tr(v0 + voff[0][1]);
-      va[4 * k2 + 3] = read_tr(v0 + voff[1][1]);
-    }
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const uint32_t x = (vb ^ (64u * cc + 32u * e)) + 1024u * e;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) va[4 * k2 + 2 * cc + e] = read_tr_at(x + 2048u * k2);
+      }
   };
   // S^T = K Q^T for 32 keys and both query blocks.
   auto qk = [&](const u32x4 (&ka)[4], SBlk& s) {
@@ -406,40 +449,47 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   // move the reference max when some lane's partial row sum is out of range
   // (the first step has already taken its max), rescale O and l, and form the weights again;
   // then fold the step's row sums into l.
-  auto settle = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
+  // Does some query of the wave need its reference max checked? Unsigned
+  // compares of the bit patterns: true for sums above the limit or above the
+  // earlier steps' sum, inf and NaN alike (the kernel is built without NaN
+  // semantics, so a float compare may not see NaN). Row sums are never
+  // negative; 2 * l is l plus one in its exponent field (l is finite, and 0
+  // before the first step).
+  auto needs_check = [&](const f32x4 (&ls)[kQB]) {
     bool need = false;
 #pragma unroll
-    // Unsigned compares of the bit patterns: true for sums above the limit or
-    // above the earlier steps' sum, inf and NaN alike (the kernel is built
-    // without NaN semantics, so a float compare may not see NaN). Row sums are
-    // never negative.
-    // 2 * l by its exponent field (l is finite, and 0 before the first step).
     for (int j = 0; j < kQB; ++j)
       need |= __builtin_bit_cast(uint32_t, ls[j][0]) >
               min(__builtin_bit_cast(uint32_t, l[j]) + 0x00800000u,
                   __builtin_bit_cast(uint32_t, kSumLimit));
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      bool moved = false;
+    return __builtin_amdgcn_ballot_w64(need) != 0;
+  };
+  // Move the reference max of every query whose step max lies above it
+  // (scaling O and l), and form the step's weights again if any query moved.
+  auto move_max = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
+    bool moved = false;
 #pragma unroll
-      for (int j = 0; j < kQB; ++j) {
-        float mr = fmaxf(s[j][0], s[j][1]);
+    for (int j = 0; j < kQB; ++j) {
+      float mr = fmaxf(s[j][0], s[j][1]);
 #pragma unroll
-        for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s[j][i]), s[j][i + 1]);  // v_max3
-        const float mx = pair_max(mr) * c;
-        if (mx > m[j]) {
-          const float alpha = __builtin_amdgcn_exp2f(m[j] - mx);
-          m[j] = mx;
-          l[j] *= alpha;
-          o[j][0] *= alpha;
-          o[j][1] *= alpha;
-          moved = true;
-        }
-      }
-      if (__builtin_amdgcn_ballot_w64(moved)) {
-        weights(s, pb);
-        row_sums(pb, ls);
+      for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s[j][i]), s[j][i + 1]);  // v_max3
+      const float mx = pair_max(mr) * c;
+      if (mx > m[j]) {
+        const float alpha = __builtin_amdgcn_exp2f(m[j] - mx);
+        m[j] = mx;
+        l[j] *= alpha;
+        o[j][0] *= alpha;
+        o[j][1] *= alpha;
+        moved = true;
       }
     }
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+      weights(s, pb);
+      row_sums(pb, ls);
+    }
+  };
+  auto settle = [&](const SBlk& s, PBlk& pb, f32x4 (&ls)[kQB]) {
+    if (needs_check(ls)) move_max(s, pb, ls);
 #pragma unroll
     for (int j = 0; j < kQB; ++j) l[j] += ls[j][0];
   };
@@ -465,16 +515,15 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
 
     // Step j: S of step j+1, weights and row sums of step j, PV of step j-1,
     // then the operand reads for the next step (K of step j+2, V of step j),
-    // then the lazy-rescale check of step j. Full steps have every part and
-    // no mask, so their body is one basic block, interleaved as groups of one
-    // MFMA and a few VALU instructions.
-    auto step = [&](auto full_tag, int j, SBlk& s_in, SBlk& s_out) __attribute__((always_inline)) {
-      constexpr bool kFull = decltype(full_tag)::value;
+    // then the lazy-rescale check of step j. This form serves the first step
+    // and the masked tail; full steps (every part present, no mask) take the
+    // pipelined form below.
+    auto part_step = [&](int j, SBlk& s_in, SBlk& s_out) __attribute__((always_inline)) {
       // P V of step j-1 first: its weights' registers are then free for step j's.
-      if (kFull || j >= 1) pv(va, pb);
-      if (kFull || j + 1 < nh) qk(ka, s_out);
-      if (!kFull && j >= first_masked) mask_step(j, s_in);
-      if (!kFull && j == 0) {
+      if (j >= 1) pv(va, pb);
+      if (j + 1 < nh) qk(ka, s_out);
+      if (j >= first_masked) mask_step(j, s_in);
+      if (j == 0) {
         // First step: take the reference max from the (masked) scores of the
         // first two steps now (those of step 1 were just issued above), so the
         // weights of both are formed against their exact max and once.
@@ -495,39 +544,100 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       }
       weights(s_in, pb);
       row_sums(pb, ls);
-      if (kFull || j + 2 < nh) kfetch(j + 2, ka);
+      if (j + 2 < nh) kfetch(j + 2, ka);
       vfetch(j, va);
-      if constexpr (kFull) {
-        // 16 S/PV MFMAs spread over the softmax, then the 4 row-sum MFMAs
-        // (they need the last weights), with the LDS reads in between.
-#pragma unroll
-        for (int i = 0; i < 4 * kQB; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
-        }
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);    // DS read
-#pragma unroll
-        for (int i = 0; i < 4 * kQB; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-        for (int i = 0; i < 2 * kQB; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
-        }
-      }
       __builtin_amdgcn_sched_barrier(0);
       settle(s_in, pb, ls);
       __builtin_amdgcn_sched_barrier(0);
     };
+
+    // Full step j, software-pipelined. Slot n (0 <= n < 8*QB) issues one
+    // 32x32x16 MFMA -- P V of step j-1 for n < 4*QB, S of step j+1 after --
+    // and then the VALU work assigned to it. The weights of step j form in
+    // 8*QB units of two scores (one packed f16 register): unit u's FMAs run in
+    // slot pipe_fma_slot(u), its exp2 one slot later and its pack one slot
+    // after that, so no instruction waits on the result of the one before it
+    // (as a chain FMA -> exp2 -> pack through two temporaries would, on the
+    // exp2 latency, with the matrix pipe idle meanwhile). S of step j is
+    // overwritten in place: its registers hold the weights in f32 until they
+    // are packed. The rare rescale path computes S again from the K tile,
+    // still in LDS, with the same MFMAs in the same order (bit for bit the
+    // same scores). A sched_barrier ends each slot, so its instructions stay
+    // together.
+    auto full_step = [&](int j, SBlk& s, SBlk& s_next) __attribute__((always_inline)) {
+      const uint32_t kb2 = k_base(j + 2);
+#pragma unroll
+      for (int n = 0; n < kSlots<kQB>(); ++n) {
+        if (n < 4 * kQB) {
+          const int jb = n >> 2, k2 = (n >> 1) & 1, hf = n & 1;
+          const u32x2 v0 = va[4 * k2 + 2 * hf], v1 = va[4 * k2 + 2 * hf + 1];
+          o[jb][hf] = mfma_f16(u32x4{v0.x, v0.y, v1.x, v1.y}, pb[jb][k2], o[jb][hf]);
+        } else {
+          const int qn = n - 4 * kQB;
+          const int dk = WRS_QK_SEQ ? qn % 4 : qn / kQB, jb = WRS_QK_SEQ ? qn / 4 : qn % kQB;
+          s_next[jb] = Elem<T>::mfma(ka[dk], qf[jb][dk], dk == 0 ? f32x16{} : s_next[jb]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8 * kQB; ++u) {
+          const int jb = u >> 3, k2 = (u >> 2) & 1, w = u & 3, i = 8 * k2 + 2 * w;
+          if (pipe_fma_slot(u) + 2 == n) {
+            const f32x2 pp = {s[jb][i], s[jb][i + 1]};
+            pb[jb][k2][w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pp, f16x2));
+          }
+          if (pipe_fma_slot(u) + 1 == n) {
+            s[jb][i] = __builtin_amdgcn_exp2f(s[jb][i]);
+            s[jb][i + 1] = __builtin_amdgcn_exp2f(s[jb][i + 1]);
+          }
+          if (pipe_fma_slot(u) == n) {
+            s[jb][i] = __builtin_fmaf(s[jb][i], c, -m[jb]);
+            s[jb][i + 1] = __builtin_fmaf(s[jb][i + 1], c, -m[jb]);
+          }
+        }
+#pragma unroll
+        for (int jb = 0; jb < kQB; ++jb) {
+          if (pipe_rowsum_slot(jb) == n) {
+            const f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                rs_sel, __builtin_bit_cast(f16x8, pb[jb][0]), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            ls[jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                rs_sel, __builtin_bit_cast(f16x8, pb[jb][1]), acc, 0, 0, 0);
+          }
+        }
+        // Operand reads for later steps, each after the last MFMA that reads
+        // the registers it fills: V of step j once P V is issued, K of step
+        // j+2 chunk by chunk behind the S MFMAs.
+        if (n == 4 * kQB) vfetch(j, va);
+#pragma unroll
+        for (int dk = 0; dk < 3; ++dk)
+          if (n == 4 * kQB + (dk + 1) * kQB)
+            ka[dk] = lds_read16(kb2 ^ (32u * dk));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      ka[3] = lds_read16(kb2 ^ 96u);
+      if (needs_check(ls)) {
+        // K of step j into the operand registers, then K of step j+2 again.
+        kfetch(j, ka);
+        qk(ka, s);
+        kfetch(j + 2, ka);
+        move_max(s, pb, ls);
+      }
+#pragma unroll
+      for (int jb = 0; jb < kQB; ++jb) l[jb] += ls[jb][0];
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto step = [&](auto full_tag, int j, SBlk& s_in, SBlk& s_out) __attribute__((always_inline)) {
+      if constexpr (decltype(full_tag)::value)
+        full_step(j, s_in, s_out);
+      else
+        part_step(j, s_in, s_out);
+    };
     typedef std::integral_constant<bool, true> Full;
     typedef std::integral_constant<bool, false> Part;
 
+
     // Tile t covers steps 2t and 2t+1, which read tiles t and t+1. Tile t+3
     // is issued into the buffer of tile t-1 (free since the last barrier);
-    // tile t+2 lands and is converted before the barrier that ends tile t.
+    // tile t+2 lands and is converted before the barrier that ends tile t,
+    // while tile t+3 stays in flight.
     auto tile = [&](auto full_tag, int t) __attribute__((always_inline)) {
       const bool more = t + 3 < n_tiles;
       if (more) issue_tile(t + 3);
@@ -535,7 +645,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       step(full_tag, 2 * t + 1, sb, sa);
       if (t + 2 < n_tiles && t > 0) {
         if (more)
-          wait_tiles<4>();
+          wait_tiles<kDmaPerTile>();
         else
           wait_tiles<0>();
         convert_tile(t + 2);
@@ -629,20 +739,22 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   }
 }
 
-// Resident 256-thread workgroups of this kernel on the current device (two per
-// CU), read once.
-int64_t small_grid_limit() {
-  static const int64_t limit = [] {
-    int dev = 0, cus = 256;
+// Compute units of the current device, read once.
+int64_t device_cus() {
+  static const int64_t cus = [] {
+    int dev = 0, n = 256;
     if (hipGetDevice(&dev) == hipSuccess)
-      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    return static_cast<int64_t>(2) * cus;
+      (void)hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    return static_cast<int64_t>(n);
   }();
-  return limit;
+  return cus;
 }
 
 template <int QB>
-hipError_t launch_qb(const PrefillArgs& a, DType dt, int64_t nwg, int n_qblk, hipStream_t s) {
+hipError_t launch_qb(const PrefillArgs& a, DType dt, hipStream_t s) {
+  constexpr int kM = queries_per_wg<QB>();
+  const int n_qblk = (a.t_q + kM - 1) / kM;
+  const int64_t nwg = n_qblk * static_cast<int64_t>(a.n_heads) * a.batch;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads);
   if (dt == kF16)
@@ -665,23 +777,17 @@ bool prefill_mfma16_supports(const PrefillArgs& a) {
 
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) {
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
+  const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
+  if (bh <= 0 || a.t_q <= 0) return hipSuccess;
   // 256-query workgroups, unless that grid fills less than one round of the
   // device's resident slots (two per CU): then 128-query workgroups, so more
-  // CUs run two workgroups (two waves per SIMD issue the softmax VALU work
-  // about twice as fast as one).
-  constexpr int kM2 = queries_per_wg<2>(), kM1 = queries_per_wg<1>();
-  const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
-  const int n_qblk2 = (a.t_q + kM2 - 1) / kM2;
-  const int64_t nwg2 = n_qblk2 * bh;
-  if (nwg2 <= 0) return hipSuccess;
-  // WRS_PREFILL_QUERIES=128 or 256 forces one schedule (tests, measurements).
-  const char* force = std::getenv("WRS_PREFILL_QUERIES");
-  const int forced = force ? std::atoi(force) : 0;
-  if (forced == kM1 || (forced != kM2 && nwg2 < small_grid_limit())) {
-    const int n_qblk1 = (a.t_q + kM1 - 1) / kM1;
-    return launch_qb<1>(a, dt, n_qblk1 * bh, n_qblk1, s);
-  }
-  return launch_qb<2>(a, dt, nwg2, n_qblk2, s);
+  // CUs run two workgroups (two waves per SIMD overlap the softmax VALU work
+  // with the matrix pipe). a.force_queries (128 or 256) forces one schedule.
+  constexpr int kM2 = queries_per_wg<2>();
+  const int64_t nwg2 = ((a.t_q + kM2 - 1) / kM2) * bh;
+  if (a.force_queries == 256 || (a.force_queries == 0 && nwg2 >= 2 * device_cus()))
+    return launch_qb<2>(a, dt, s);
+  return launch_qb<1>(a, dt, s);
 }
 
 }  // namespace wrs

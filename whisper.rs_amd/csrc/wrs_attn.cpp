@@ -44,6 +44,9 @@ struct wrs_attn_ctx {
   size_t lin_x_bytes = 0;
   float* ln_x = nullptr;  // fused projections above the weight-stream size: normalized rows
   size_t ln_x_bytes = 0;
+  // Prefill schedule overrides (wrs_attn_set_schedule).
+  int prefill_queries = 0;
+  int f32_split = -1;
 };
 
 struct wrs_kv {
@@ -219,6 +222,8 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
   a.causal = causal ? 1 : 0;
   a.q_pos_offset = static_cast<int>(q_pos_offset);
   a.scale = 1.0f / std::sqrt(static_cast<float>(d_head));
+  a.force_queries = c->prefill_queries;
+  a.force_f32_split = c->f32_split;
 
   if (t_kv == 0) {
     // attention.rs:93-96: zero output. Rows of out may be strided.
@@ -437,6 +442,18 @@ int wrs_attn_set_stream(wrs_attn_ctx* c, void* s) {
 }
 
 void* wrs_attn_get_stream(wrs_attn_ctx* c) { return c ? c->stream : nullptr; }
+
+int wrs_attn_set_schedule(wrs_attn_ctx* c, int prefill_queries, int f32_split) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (prefill_queries != 0 && prefill_queries != 128 && prefill_queries != 256)
+    return fail(c, WRS_EINVAL, "prefill_queries must be 0, 128 or 256");
+  if (f32_split < -1 || f32_split > 4)
+    return fail(c, WRS_EINVAL, "f32_split must be -1..4");
+  c->prefill_queries = prefill_queries;
+  c->f32_split = f32_split;
+  return WRS_OK;
+}
 
 int wrs_attn_synchronize(wrs_attn_ctx* c) {
   if (!c) return WRS_EINVAL;

@@ -46,6 +46,12 @@ struct PrefillArgs {
   int causal;        // mask keys j > i + q_pos_offset
   int q_pos_offset;  // absolute position of query row 0 (decoder prompt: t_past)
   float scale;       // 1/sqrt(d_head), rounded to f32 like attention.rs:107
+  // Schedule overrides from the context (wrs_attn_set_schedule): queries per
+  // workgroup of the 16-bit kernel (0 = by grid size), and the f32 kernel's
+  // key split (-1 = by grid size, 0 = 128-query blocks, 1 = four waves,
+  // 2..4 = that many waves).
+  int force_queries;
+  int force_f32_split;
 };
 
 // MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type, rows 16-byte
