@@ -187,12 +187,19 @@ def _replay_time_us(g, reps, launches_per_replay):
     return start.elapsed_time(end) * 1e3 / (reps * launches_per_replay)
 
 
+# Launch shapes of the read-floor sweep: (threads per workgroup, 16-byte
+# loads per lane), from 1875 down to 40 workgroups for 7.68 MB.
+FLOOR_SHAPES = ((256, 1), (256, 4), (256, 8), (512, 2), (512, 4), (512, 8), (1024, 2),
+                (1024, 4), (512, 24))
+
+
 def bench_decode(wrs, W, ctx, reps, use_graph=True):
     """Cross-attention decode, one launch per layer over 32 resident layers,
     three utterances' caches rotated (737 MB > the 256 MB MALL), replayed
     from a HIP graph. Beside it, the practical floor of one decode-sized
-    launch: a plain streaming read of the same 7.68 MB per launch
-    (wrs_stream_read), rotated the same way."""
+    launch: a plain streaming read of the same 7.68 MB per launch, rotated
+    the same way, at the fastest of several launch shapes
+    (wrs_stream_read_shape)."""
     import torch
     cfg = W.LARGE_CROSS_DECODE
     U = 3  # utterances rotated: 3 x 245.76 MB of cross K/V > 256 MB MALL
@@ -236,48 +243,47 @@ def bench_decode(wrs, W, ctx, reps, use_graph=True):
     log(f"decode: timing {reps} graph replays of {U * cfg.n_layers} launches")
     us = _replay_time_us(g, reps, U * cfg.n_layers)
     gbs = cfg.bytes_per_layer() / (us * 1e-6) / 1e9
-    # the floor: 7.68 MB per launch (two layers' K planes, contiguous)
+    # The floor: 7.68 MB per launch (two layers' K planes, contiguous), read
+    # once by a plain streaming kernel, rotated like the decode, over launch
+    # shapes from 40 to 1875 workgroups; the fastest shape is the floor.
     per = 2 * cfg.n_heads * cfg.n_audio * 64 * 2
-    sink = torch.zeros(per // 32768 + 1, device="cuda")
+    sink = torch.zeros(per // 4096 + 1, device="cuda")
     bases = [ar.plane_pointers()[2] for ar in arenas]
 
-    def all_reads():
-        for base in bases:
-            for pair in range(cfg.n_layers // 2):
-                ctx.check(ctx._lib.wrs_stream_read(ctx.handle, base + pair * per, per,
-                                                   sink.data_ptr(), sink.numel()),
-                          "wrs_stream_read")
+    def reads(threads, loads, nbytes):
+        def fn():
+            for base in bases:
+                for pair in range(cfg.n_layers // 2):
+                    ctx.check(ctx._lib.wrs_stream_read_shape(
+                        ctx.handle, base + pair * per, nbytes, threads, loads, sink.data_ptr(),
+                        sink.numel()), "wrs_stream_read_shape")
+        return fn
 
-    all_reads()
-    torch.cuda.synchronize()
-    gf = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gf):
+    def replay_us(fn):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            ctx.use_torch_stream()
+            fn()
         ctx.use_torch_stream()
-        all_reads()
-    ctx.use_torch_stream()
-    floor_us = _replay_time_us(gf, reps, U * cfg.n_layers // 2)
-    # and what any launch costs in these replays: the same kernel over 16 bytes
-    # (one workgroup: one load, one store)
-    def all_tiny():
-        for base in bases:
-            for pair in range(cfg.n_layers // 2):
-                ctx.check(ctx._lib.wrs_stream_read(ctx.handle, base + pair * per, 16,
-                                                   sink.data_ptr(), sink.numel()),
-                          "wrs_stream_read")
+        return _replay_time_us(gr, reps, U * cfg.n_layers // 2)
 
-    all_tiny()
-    torch.cuda.synchronize()
-    gt = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gt):
-        ctx.use_torch_stream()
-        all_tiny()
-    ctx.use_torch_stream()
-    tiny_us = _replay_time_us(gt, reps, U * cfg.n_layers // 2)
-    floor = {"bytes_per_launch": per, "us_per_launch": round(floor_us, 3),
+    shapes = {}
+    for threads, loads in FLOOR_SHAPES:
+        shapes[f"{threads}x{loads}"] = {
+            "workgroups": -(-per // (16 * threads * loads)),
+            "us_per_launch": round(replay_us(reads(threads, loads, per)), 3)}
+    best = min(shapes, key=lambda k: shapes[k]["us_per_launch"])
+    floor_us = shapes[best]["us_per_launch"]
+    # and what any launch costs in these replays: one workgroup, one load
+    tiny_us = replay_us(reads(256, 1, 16))
+    floor = {"bytes_per_launch": per, "us_per_launch": floor_us,
              "GBps": round(per / (floor_us * 1e-6) / 1e9, 1),
-             "one_workgroup_launch_us": round(tiny_us, 3)}
+             "best_shape": best + " (threads x 16-byte loads per lane)",
+             "shapes": shapes, "one_workgroup_launch_us": round(tiny_us, 3)}
     log(f"decode: {us:.3f} us/launch ({gbs:.1f} GB/s); single-launch read floor "
-        f"{floor_us:.3f} us ({floor['GBps']} GB/s); one-workgroup launch {tiny_us:.3f} us")
+        f"{floor_us:.3f} us ({floor['GBps']} GB/s, {best}); one-workgroup launch {tiny_us:.3f} us")
     for ar in arenas:
         ar.close()
     return cfg, us, gbs, floor
@@ -343,6 +349,44 @@ def bench_decode_self(wrs, W, ctx, reps, lengths=None, eager=False):
         res[L] = {"us_per_launch": round(us, 3), "GBps": round(gbs, 1),
                   "bytes_per_launch": cfg.bytes(), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
         log(f"decode self L={L}: {us:.3f} us/launch, {gbs:.1f} GB/s")
+    if not eager:
+        # The read floor at the headline length: the same bytes per launch,
+        # contiguous, read once by a plain streaming kernel at its fastest
+        # shape, rotated over the arenas and layers like the decode.
+        L0 = base.ctx
+        per = (W.SelfDecode(base.name, base.beams, base.n_heads, L0).bytes() + 15) // 16 * 16
+        # the read windows stay inside each arena's self K planes
+        k_plane_bytes = n_layers * base.beams * base.n_heads * maxc * 64 * 2
+        n_fit = k_plane_bytes // per
+        assert n_fit >= 1
+        sink = torch.zeros(per // 4096 + 1, device="cuda")
+        bases = [ar.plane_pointers()[0] for ar in arenas]
+
+        def reads(threads, loads):
+            def fn():
+                for bp in bases:
+                    for layer in range(n_layers):
+                        ctx.check(ctx._lib.wrs_stream_read_shape(
+                            ctx.handle, bp + (layer % n_fit) * per, per, threads, loads,
+                            sink.data_ptr(), sink.numel()), "wrs_stream_read_shape")
+            return fn
+
+        best = None
+        for threads, loads in ((256, 1), (256, 4), (512, 2), (512, 4)):
+            fn = reads(threads, loads)
+            fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                ctx.use_torch_stream()
+                fn()
+            ctx.use_torch_stream()
+            t = _replay_time_us(gr, reps, U * n_layers)
+            if best is None or t < best[0]:
+                best = (t, f"{threads}x{loads}")
+        res["floor"] = {"length": L0, "bytes_per_launch": per, "us_per_launch": round(best[0], 3),
+                        "best_shape": best[1] + " (threads x 16-byte loads per lane)"}
+        log(f"decode self: read floor at L={L0}: {best[0]:.3f} us ({best[1]})")
     for ar in arenas:
         ar.close()
     return res
@@ -614,18 +658,27 @@ def bench_rows(wrs, ctx, reps):
     """LayerNorm over the large-v3 encoder rows of 16 windows (24000 x 1280 f32
     in, bf16 out, encoder.rs:266-274) and GELU over their MLP activations
     (24000 x 5120 f32 in place): HBM-bound, algorithmic bytes = one read and
-    one write."""
+    one write. LayerNorm's 184 MB per call would fit the 256 MB MALL, so its
+    calls rotate over four input/output pairs (737 MB); GELU's 491 MB working
+    set does not fit."""
     import torch
     gen = torch.Generator(device="cuda").manual_seed(0x5EED)
     T, d = 24000, 1280
-    x = torch.randn((T, d), generator=gen, device="cuda")
+    n_rot = 4
+    xs = [torch.randn((T, d), generator=gen, device="cuda") for _ in range(n_rot)]
     g = torch.randn(d, generator=gen, device="cuda")
     b = torch.randn(d, generator=gen, device="cuda")
-    y = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    ys = [torch.empty((T, d), dtype=torch.bfloat16, device="cuda") for _ in range(n_rot)]
     h = torch.randn((T, 4 * d), generator=gen, device="cuda")
+    turn = [0]
+
+    def layer_norm():
+        i = turn[0] % n_rot
+        turn[0] += 1
+        wrs.layer_norm(xs[i], g, b, 1e-5, ys[i], ctx=ctx)
+
     res = {}
-    for name, fn, nbytes in (("layer_norm", lambda: wrs.layer_norm(x, g, b, 1e-5, y, ctx=ctx),
-                              T * d * (4 + 2)),
+    for name, fn, nbytes in (("layer_norm", layer_norm, T * d * (4 + 2)),
                              ("gelu", lambda: wrs.gelu_inplace(h, ctx=ctx), T * 4 * d * 8)):
         for _ in range(20):
             fn()
@@ -1084,6 +1137,7 @@ def main():
         cpu["stream"] = cpu_baseline_stream(scfg, n)
 
     L0 = W.SMALL_SELF_DECODE.ctx
+    self_floor = sweep.pop("floor", None)
     self_ref = sweep[L0]
     line = {
         "metric": METRIC,
@@ -1130,6 +1184,9 @@ def main():
             "roofline": _roof(self_ref["GBps"], PEAK_HBM_GBS, "GB/s", "hbm",
                               traffic_bytes("decode_self")),
             "sweep": {str(L): v for L, v in sweep.items()},
+            "single_launch_read_floor": self_floor,
+            "frac_of_read_floor": (round(self_floor["us_per_launch"] / self_ref["us_per_launch"], 4)
+                                   if self_floor else None),
             "cpu_baseline": cpu.get("decode_self"),
         },
         "capture": {

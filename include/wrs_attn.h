@@ -33,6 +33,7 @@ extern "C" {
 #define WRS_EUNSUPPORTED (-4) /* valid for the reference, not handled on the GPU */
 #define WRS_ERANGE (-5)      /* layer/slot index or length outside the arena */
 #define WRS_ECAPTURE (-6)    /* context scratch would grow while the stream records a graph */
+#define WRS_EBUSY (-7)       /* every slot of the GPU's fixed scratch is held by other contexts */
 
 /* Element types of device-resident tensors. */
 #define WRS_F32 0
@@ -59,7 +60,10 @@ typedef struct wrs_layout {
 int wrs_attn_create(int device, wrs_attn_ctx **out);
 void wrs_attn_destroy(wrs_attn_ctx *ctx);
 /* Queue work on a caller-owned hipStream_t; NULL is the device's null
- * (default) stream. A new context starts on a stream of its own. */
+ * (default) stream. A new context starts on a stream of its own. The switch
+ * drains the previous stream (unless either stream records a graph), so the
+ * previous stream must still exist: before destroying a stream the context
+ * uses, switch the context to another stream or to NULL. */
 int wrs_attn_set_stream(wrs_attn_ctx *ctx, void *hip_stream);
 void *wrs_attn_get_stream(wrs_attn_ctx *ctx);
 int wrs_attn_synchronize(wrs_attn_ctx *ctx);
@@ -208,17 +212,21 @@ int wrs_attn_decode_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const size
  * A layer without cross K/V (never set, invalidated, or an arena created with
  * n_audio_max = 0) gives zero rows, as t_kv == 0 does (attention.rs:93-96). */
 int wrs_attn_decode_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
-                          size_t n_beams, float *out);
+                          size_t n_beams, float *out); /* q 16-byte aligned */
 /* Allocation-free variant of wrs_attn_decode_cross, with the same arguments
  * and results. No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Its split-K partials and merge counters
- * live in a fixed device array of the library (2 MiB + 64 KiB, one per GPU,
- * held until the process ends), so it never calls hipMalloc or hipFree; a
- * shape whose partials do not fit (beams x heads x ceil(n_audio / 128) x 68
- * floats above 524288, or more than 16384 heads) fails with WRS_ERANGE. Every
- * call on one GPU shares that array: calls that overlap on one GPU (other
- * streams, other contexts) race. */
+ * live in a fixed device array of the library (4 slots of 512 KiB + 16 KiB,
+ * one array per GPU, held until the process ends), so it never calls
+ * hipMalloc or hipFree. A context claims one slot of its GPU on its first
+ * call here and releases it in wrs_attn_destroy; with all four held by other
+ * live contexts the call fails with WRS_EBUSY. Limits per call: at most 128
+ * heads, and for n_audio above 256 (shorter planes need no partials)
+ * min(n_beams, 8) x n_heads x ceil(n_audio / 128) x 68 <= 131072 floats
+ * (large-v3: up to 8 beams); larger shapes fail with WRS_ERANGE. q must be
+ * 16-byte aligned (WRS_EINVAL otherwise). Calls of one context are ordered on
+ * its stream; two contexts never share a slot. */
 int wrs_attn_decode_cross_noalloc(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
                                   size_t n_beams, float *out);
 /* Multi-token rows (prompt prefill): decoder.rs:857-891 self-attention with
@@ -229,7 +237,7 @@ int wrs_attn_decode_cross_noalloc(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, c
 int wrs_attn_prefill_self(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, size_t slot,
                           const float *q, size_t n_tokens, float *out);
 int wrs_attn_prefill_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
-                           size_t n_tokens, float *out);
+                           size_t n_tokens, float *out); /* q 16-byte aligned */
 /* wrs_attn_prefill_cross (the multi_head_attention call of decoder.rs:698-708)
  * that also writes each row's softmax statistics for
  * wrs_attn_capture_cross_heads_lse: lse is an f32
@@ -238,7 +246,7 @@ int wrs_attn_prefill_cross(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const fl
  * sum = sum_j exp2(log2(e) * s_ij - max), s_ij = q_i.k_j / 8. Not written when
  * the layer has no cross keys. */
 int wrs_attn_prefill_cross_lse(wrs_attn_ctx *ctx, wrs_kv *kv, size_t layer, const float *q,
-                               size_t n_tokens, float *out, float *lse);
+                               size_t n_tokens, float *out, float *lse); /* q 16-byte aligned */
 
 /* ---- alignment-head capture (asynchronous) -----------------------------
  * fn capture_cross_attention_heads(q, k, n_tokens, n_audio, n_heads, d_model,
@@ -350,6 +358,12 @@ int wrs_kv_set_cross_proj(wrs_kv *kv, int x_dtype, const void *enc, size_t enc_l
  * Asynchronous. */
 int wrs_stream_read(wrs_attn_ctx *ctx, const void *src, size_t bytes, float *sink,
                     size_t sink_len);
+/* The same read with another launch shape: `threads` per workgroup (256,
+ * 512 or 1024) and `loads_per_lane` 16-byte loads per lane (1, 2, 4, 8, 16
+ * or 24), all issued before any is used; sink_len >= ceil(bytes /
+ * (16 * threads * loads_per_lane)). Other shapes: WRS_EINVAL. Asynchronous. */
+int wrs_stream_read_shape(wrs_attn_ctx *ctx, const void *src, size_t bytes, int threads,
+                          int loads_per_lane, float *sink, size_t sink_len);
 
 #ifdef __cplusplus
 }

@@ -71,6 +71,7 @@ pub mod ffi {
     pub const WRS_EUNSUPPORTED: c_int = -4;
     pub const WRS_ERANGE: c_int = -5;
     pub const WRS_ECAPTURE: c_int = -6;
+    pub const WRS_EBUSY: c_int = -7;
 
     pub const WRS_F32: c_int = 0;
     pub const WRS_F16: c_int = 1;
@@ -203,6 +204,8 @@ pub mod ffi {
         // measurement helper (no reference counterpart)
         pub fn wrs_stream_read(ctx: *mut WrsCtx, src: *const c_void, bytes: usize,
             sink: *mut f32, sink_len: usize) -> c_int;
+        pub fn wrs_stream_read_shape(ctx: *mut WrsCtx, src: *const c_void, bytes: usize,
+            threads: c_int, loads_per_lane: c_int, sink: *mut f32, sink_len: usize) -> c_int;
     }
 }
 

@@ -25,6 +25,7 @@ WRS_EHIP = -3
 WRS_EUNSUPPORTED = -4
 WRS_ERANGE = -5
 WRS_ECAPTURE = -6
+WRS_EBUSY = -7
 
 WRS_F32 = 0
 WRS_F16 = 1
@@ -63,6 +64,7 @@ _SIGNATURES = {
     "wrs_attn_status_string": (ctypes.c_char_p, [_int]),
     "wrs_attn_reserve": (_int, [_vp, ctypes.POINTER(Reserve)]),
     "wrs_stream_read": (_int, [_vp, _vp, _sz, _vp, _sz]),
+    "wrs_stream_read_shape": (_int, [_vp, _vp, _sz, _int, _int, _vp, _sz]),
     "wrs_flash_attention_2": (_int, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz, _int,
                                      _vp, _sz]),
     "wrs_multi_head_attention": (_int, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,

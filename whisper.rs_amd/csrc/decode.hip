@@ -493,7 +493,59 @@ __global__ __launch_bounds__(512) void stream_read(const u32x4* src, int64_t n16
   }
 }
 
+// The same with a chosen shape: T threads per workgroup, L 16-byte loads per
+// lane (lane i of workgroup b reads chunks b*T*L + i + T*j), all issued before
+// any is used.
+template <int T, int L>
+__global__ __launch_bounds__(T) void stream_read_shape(const u32x4* src, int64_t n16, float* sink) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * T * L + threadIdx.x;
+  u32x4 x[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const int64_t idx = base + static_cast<int64_t>(T) * i;
+    x[i] = idx < n16 ? src[idx] : u32x4{0, 0, 0, 0};
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < L; ++i) acc ^= x[i].x ^ x[i].y ^ x[i].z ^ x[i].w;
+  __shared__ uint32_t red[T / 64];
+  for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+    for (int w = 0; w < T / 64; ++w) r ^= red[w];
+    sink[blockIdx.x] = __builtin_bit_cast(float, r & 0x3fffffffu);
+  }
+}
+
 }  // namespace
+
+int64_t stream_read_shape_blocks(int64_t bytes, int threads, int loads) {
+  const int64_t per = static_cast<int64_t>(threads) * loads;
+  return per > 0 ? (bytes / 16 + per - 1) / per : 0;
+}
+
+hipError_t launch_stream_read_shape(const void* src, int64_t bytes, int threads, int loads,
+                                    float* sink, hipStream_t s) {
+  const int64_t n16 = bytes / 16;
+  const int64_t blocks = stream_read_shape_blocks(bytes, threads, loads);
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const u32x4* p = static_cast<const u32x4*>(src);
+#define WRS_SRS(T, L)                                                             \
+  if (threads == T && loads == L) {                                               \
+    hipLaunchKernelGGL((stream_read_shape<T, L>), grid, dim3(T), 0, s, p, n16, sink); \
+    return hipGetLastError();                                                     \
+  }
+  WRS_SRS(256, 1) WRS_SRS(256, 2) WRS_SRS(256, 4) WRS_SRS(256, 8) WRS_SRS(256, 16) WRS_SRS(256, 24)
+  WRS_SRS(512, 1) WRS_SRS(512, 2) WRS_SRS(512, 4) WRS_SRS(512, 8) WRS_SRS(512, 16) WRS_SRS(512, 24)
+  WRS_SRS(1024, 1) WRS_SRS(1024, 2) WRS_SRS(1024, 4) WRS_SRS(1024, 8) WRS_SRS(1024, 16)
+  WRS_SRS(1024, 24)
+#undef WRS_SRS
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_stream_read(const void* src, int64_t bytes, float* sink, hipStream_t s) {
   const int64_t n16 = bytes / 16;

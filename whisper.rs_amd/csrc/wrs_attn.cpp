@@ -18,12 +18,16 @@
 using wrs::DType;
 
 // Fixed scratch of the allocation-free cross decode
-// (wrs_attn_decode_cross_noalloc): f32 split-K partials, then the merge
-// counters. Each GPU the library runs on holds its own copy until the process
-// ends; every call on that GPU shares it, so such calls must not overlap.
-constexpr size_t kNoallocPartBytes = size_t{2} << 20;       // 524288 f32 partials
-constexpr size_t kNoallocCounterBytes = size_t{64} << 10;   // 16384 counter words
-static __device__ __align__(256) unsigned char scratch[kNoallocPartBytes + kNoallocCounterBytes];
+// (wrs_attn_decode_cross_noalloc): kNoallocSlots slots, each f32 split-K
+// partials followed by merge counters. Each GPU the library runs on holds its
+// own copy until the process ends. A context claims one slot of its GPU on its
+// first allocation-free call and releases it when destroyed, so the calls of
+// different contexts never share partials or counters.
+constexpr int kNoallocSlots = 4;
+constexpr size_t kNoallocPartBytes = size_t{512} << 10;     // 131072 f32 partials per slot
+constexpr size_t kNoallocCounterBytes = size_t{16} << 10;   // 128 counter lines per slot
+constexpr size_t kNoallocSlotBytes = kNoallocPartBytes + kNoallocCounterBytes;
+static __device__ __align__(256) unsigned char scratch[kNoallocSlots * kNoallocSlotBytes];
 
 struct wrs_attn_ctx {
   int device = 0;
@@ -47,6 +51,9 @@ struct wrs_attn_ctx {
   // Prefill schedule overrides (wrs_attn_set_schedule).
   int prefill_queries = 0;
   int f32_split = -1;
+  // Slot of the allocation-free entry point's fixed scratch held by this
+  // context (-1: none yet).
+  int noalloc_slot = -1;
 };
 
 struct wrs_kv {
@@ -255,6 +262,7 @@ constexpr int kMaxNoallocDevices = 64;
 struct NoallocScratch {
   std::mutex mu;
   unsigned char* ptr[kMaxNoallocDevices] = {};
+  bool held[kMaxNoallocDevices][kNoallocSlots] = {};  // slots claimed by live contexts
 };
 NoallocScratch& noalloc_scratch() {
   static NoallocScratch s;
@@ -272,19 +280,50 @@ int noalloc_setup(wrs_attn_ctx* c) {
   const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !p) return fail(c, WRS_EHIP, "hipGetSymbolAddress(scratch)", e);
   unsigned char* base = static_cast<unsigned char*>(p);
-  WRS_HIP(c, wrs::launch_fill_zero_u32(reinterpret_cast<unsigned*>(base + kNoallocPartBytes),
-                                       static_cast<int64_t>(kNoallocCounterBytes / 4),
-                                       c->stream));
+  for (int k = 0; k < kNoallocSlots; ++k)
+    WRS_HIP(c, wrs::launch_fill_zero_u32(
+                   reinterpret_cast<unsigned*>(base + k * kNoallocSlotBytes + kNoallocPartBytes),
+                   static_cast<int64_t>(kNoallocCounterBytes / 4), c->stream));
   WRS_HIP(c, hipStreamSynchronize(c->stream));
   ns.ptr[c->device] = base;
   return WRS_OK;
 }
 
-unsigned char* noalloc_ptr(int device) {
-  if (device < 0 || device >= kMaxNoallocDevices) return nullptr;
+// This context's slot of the fixed scratch, claimed on first use: nullptr
+// with *rc set when the GPU has no fixed scratch or every slot is held.
+unsigned char* noalloc_slot_ptr(wrs_attn_ctx* c, int* rc) {
+  *rc = WRS_OK;
+  if (c->device < 0 || c->device >= kMaxNoallocDevices) {
+    *rc = fail(c, WRS_EUNSUPPORTED, "no fixed scratch on this device");
+    return nullptr;
+  }
   NoallocScratch& ns = noalloc_scratch();
   std::lock_guard<std::mutex> lk(ns.mu);
-  return ns.ptr[device];
+  if (!ns.ptr[c->device]) {
+    *rc = fail(c, WRS_EUNSUPPORTED, "no fixed scratch on this device");
+    return nullptr;
+  }
+  if (c->noalloc_slot < 0) {
+    for (int k = 0; k < kNoallocSlots && c->noalloc_slot < 0; ++k)
+      if (!ns.held[c->device][k]) {
+        ns.held[c->device][k] = true;
+        c->noalloc_slot = k;
+      }
+    if (c->noalloc_slot < 0) {
+      *rc = fail(c, WRS_EBUSY,
+                 "every slot of this GPU's fixed scratch is held by another context");
+      return nullptr;
+    }
+  }
+  return ns.ptr[c->device] + c->noalloc_slot * kNoallocSlotBytes;
+}
+
+void noalloc_release(wrs_attn_ctx* c) {
+  if (c->noalloc_slot < 0 || c->device < 0 || c->device >= kMaxNoallocDevices) return;
+  NoallocScratch& ns = noalloc_scratch();
+  std::lock_guard<std::mutex> lk(ns.mu);
+  ns.held[c->device][c->noalloc_slot] = false;
+  c->noalloc_slot = -1;
 }
 
 // Split-K decode over f16 planes. `fixed` (the device address of `scratch`)
@@ -335,8 +374,8 @@ int decode_impl(wrs_attn_ctx* c, const float* q, int64_t q_rs, float* out, int64
     if (fixed) {
       if (pb > kNoallocPartBytes || cb > kNoallocCounterBytes)
         return fail(c, WRS_ERANGE,
-                    "decode shape needs more than the fixed scratch (2 MiB of partials, "
-                    "64 KiB of counters)");
+                    "decode shape needs more than one slot of the fixed scratch (512 KiB of "
+                    "partials, counters for 128 heads)");
     } else {
       int rc = grow(c, reinterpret_cast<void**>(&c->part), &c->part_bytes, pb, false);
       if (rc) return rc;
@@ -379,6 +418,7 @@ const char* wrs_attn_status_string(int status) {
     case WRS_EUNSUPPORTED: return "unsupported on the GPU path";
     case WRS_ERANGE: return "index or length outside the arena";
     case WRS_ECAPTURE: return "scratch would grow during graph capture (reserve it first)";
+    case WRS_EBUSY: return "every slot of the fixed scratch is held by another context";
     default: return "unknown status";
   }
 }
@@ -397,12 +437,10 @@ int wrs_attn_create(int device, wrs_attn_ctx** out) {
     return WRS_EHIP;
   }
   c->stream = c->own_stream;
-  const int rc = noalloc_setup(c);
-  if (rc) {
-    (void)hipStreamDestroy(c->own_stream);
-    delete c;
-    return rc;
-  }
+  // The fixed scratch serves only the allocation-free entry point: if it
+  // cannot be set up, the context still serves every other call and that
+  // entry point returns WRS_EUNSUPPORTED.
+  if (noalloc_setup(c) != WRS_OK) c->err.clear();
   *out = c;
   return WRS_OK;
 }
@@ -418,6 +456,7 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
   if (c->lin_x) (void)hipFree(c->lin_x);
   if (c->ln_x) (void)hipFree(c->ln_x);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  noalloc_release(c);  // the stream is drained: no call uses the slot any more
   delete c;
 }
 
@@ -476,6 +515,27 @@ int wrs_stream_read(wrs_attn_ctx* c, const void* src, size_t bytes, float* sink,
     return fail(c, WRS_EINVAL, "stream_read: sink shorter than one float per workgroup");
   DeviceGuard g(c->device);
   WRS_HIP(c, wrs::launch_stream_read(src, static_cast<int64_t>(bytes), sink, c->stream));
+  return WRS_OK;
+}
+
+int wrs_stream_read_shape(wrs_attn_ctx* c, const void* src, size_t bytes, int threads,
+                          int loads_per_lane, float* sink, size_t sink_len) {
+  if (!c) return WRS_EINVAL;
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (bytes == 0) return WRS_OK;
+  if (!src || !sink) return fail(c, WRS_EINVAL, "null argument");
+  if (bytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15))
+    return fail(c, WRS_EINVAL, "stream_read_shape: 16-byte aligned multiple of 16 bytes");
+  if ((threads != 256 && threads != 512 && threads != 1024) ||
+      (loads_per_lane != 1 && loads_per_lane != 2 && loads_per_lane != 4 && loads_per_lane != 8 &&
+       loads_per_lane != 16 && loads_per_lane != 24))
+    return fail(c, WRS_EINVAL, "stream_read_shape: threads 256/512/1024, loads 1/2/4/8/16/24");
+  if (sink_len < static_cast<size_t>(wrs::stream_read_shape_blocks(static_cast<int64_t>(bytes),
+                                                                   threads, loads_per_lane)))
+    return fail(c, WRS_EINVAL, "stream_read_shape: sink shorter than one float per workgroup");
+  DeviceGuard g(c->device);
+  WRS_HIP(c, wrs::launch_stream_read_shape(src, static_cast<int64_t>(bytes), threads,
+                                           loads_per_lane, sink, c->stream));
   return WRS_OK;
 }
 
@@ -957,6 +1017,8 @@ int decode_cross_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
   if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
   if (n_beams == 0) return WRS_OK;
   if (!q || !out) return fail(c, WRS_EINVAL, "null argument");
+  if (reinterpret_cast<uintptr_t>(q) & 15)
+    return fail(c, WRS_EINVAL, "q must be 16-byte aligned");
   DeviceGuard g(c->device);
   const int64_t dm = static_cast<int64_t>(kv->d_model());
   const size_t L = kv->cross_len[layer];
@@ -990,6 +1052,8 @@ int cross_rows_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, s
   if (layer >= kv->n_layers) return fail(c, WRS_ERANGE, "layer out of range");
   if (n == 0) return WRS_OK;
   if (!q || !out) return fail(c, WRS_EINVAL, "null argument");
+  if (reinterpret_cast<uintptr_t>(q) & 15)
+    return fail(c, WRS_EINVAL, "q must be 16-byte aligned");
   if (!fits_int(n)) return fail(c, WRS_EINVAL, "dimension exceeds 2^31");
   DeviceGuard g(c->device);
   const int64_t dm = static_cast<int64_t>(kv->d_model());
@@ -1034,8 +1098,9 @@ int wrs_attn_decode_cross_noalloc(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, con
                                   size_t n_beams, float* out) {
   if (!c || !kv) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
-  unsigned char* fixed = noalloc_ptr(c->device);
-  if (!fixed) return fail(c, WRS_EUNSUPPORTED, "no fixed scratch on this device");
+  int rc = WRS_OK;
+  unsigned char* fixed = noalloc_slot_ptr(c, &rc);
+  if (!fixed) return rc;
   return decode_cross_impl(c, kv, layer, q, n_beams, out, fixed);
 }
 

@@ -115,6 +115,11 @@ size_t decode_counter_words(int n_groups, int n_heads);
 // workgroup); sink receives stream_read_blocks(bytes) floats.
 hipError_t launch_stream_read(const void* src, int64_t bytes, float* sink, hipStream_t s);
 int64_t stream_read_blocks(int64_t bytes);
+// The same with `threads` per workgroup (256, 512, 1024) and `loads` 16-byte
+// loads per lane (1, 2, 4, 8, 16, 24).
+hipError_t launch_stream_read_shape(const void* src, int64_t bytes, int threads, int loads,
+                                    float* sink, hipStream_t s);
+int64_t stream_read_shape_blocks(int64_t bytes, int threads, int loads);
 
 // Alignment-head capture over the f16 cross plane
 // (decoder.rs:796-828 semantics): for query row i and pair p,
