@@ -752,6 +752,31 @@ def copy_bandwidth():
     return 2 * a.numel() * 4 / (ms * 1e-3) / 1e9
 
 
+def read_bandwidth(ctx):
+    """Read-only streaming rate over 1 GiB (wrs_stream_read_shape, 256 threads x
+    eight 16-byte loads per lane): the ceiling of a pure read stream, beside the
+    copy's 1:1 read/write mix."""
+    import torch
+    nbytes = 1 << 30
+    a = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    sink = torch.zeros(nbytes // (16 * 256 * 8) + 1, device="cuda")
+
+    def run():
+        ctx.check(ctx._lib.wrs_stream_read_shape(ctx.handle, a.data_ptr(), nbytes, 256, 8,
+                                                 sink.data_ptr(), sink.numel()),
+                  "wrs_stream_read_shape")
+
+    run()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(10):
+        run()
+    e.record()
+    torch.cuda.synchronize()
+    return nbytes / (s.elapsed_time(e) / 10 * 1e-3) / 1e9
+
+
 CALIB_BYTES = 256 << 20  # one plain device copy of this many bytes per profiled run
 
 
@@ -1069,6 +1094,8 @@ def main():
         return
     if args.only == "rows":
         bench_rows(wrs, ctx, args.rows_reps)
+        log(f"rows only: device copy {copy_bandwidth():.1f} GB/s, read stream "
+            f"{read_bandwidth(ctx):.1f} GB/s")
         calibration_copy()
         return
     if args.only == "stream":
@@ -1108,6 +1135,7 @@ def main():
     log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
     host_slice = bench_host_slice(wrs, W, ctx)
     copy_gbs = copy_bandwidth()
+    read_gbs = read_bandwidth(ctx)
 
     traffic = None
     if not args.no_traffic:
@@ -1222,7 +1250,7 @@ def main():
         "row_kernels": rows,
         "host_slice": host_slice,
         "device": {"name": props.name, "cu": props.multi_processor_count,
-                   "copy_GBps": round(copy_gbs, 1)},
+                   "copy_GBps": round(copy_gbs, 1), "read_GBps": round(read_gbs, 1)},
         "host": info,
     }
     print(json.dumps(line), flush=True)
