@@ -155,13 +155,32 @@ int wrs_attn_prefill(wrs_attn_ctx *ctx, int q_dtype, const void *q, const wrs_la
 
 /* ---- device KV arena ---------------------------------------------------
  * pub struct DecoderKvCache (crates/whisper/src/decoder.rs:131-145), in HBM:
- * self K/V f16 [layer][slot][head][max_ctx][64], cross K/V f16
+ * self K/V [layer][slot][head][max_ctx][64], cross K/V
  * [layer][head][n_audio_max][64]; d_head is 64, d_model = n_heads*64.
- * Slot lengths (the reference's t_past vector) are kept on the host. */
+ * Slot lengths (the reference's t_past vector) are kept on the host.
+ * Planes are f16 (wrs_kv_create: the MFMA and split-K decode kernels) or f32
+ * (wrs_kv_create_dtype with WRS_F32: the reference's own f32 cache, twice the
+ * bytes, with the reference's arithmetic -- decode, cached prompt rows and
+ * single cross rows on the exact decode kernel, as the host-slice
+ * single_token_mha_d64 / mha_with_cache run; cross prompt rows on the f32
+ * prefill kernel, as wrs_flash_attention_2 runs them; capture with f32
+ * scores). On f32 arenas wrs_attn_decode_cross_noalloc,
+ * wrs_attn_prefill_cross_lse and wrs_attn_capture_cross_heads_lse return
+ * WRS_EUNSUPPORTED, and the attention calls size their score scratch
+ * (rows x heads x keys floats) on the first call, so a first call under
+ * stream capture fails with WRS_ECAPTURE. */
 
-/* DecoderKvCache::new (decoder.rs:148-157) with the arena capacity fixed. */
+/* DecoderKvCache::new (decoder.rs:148-157) with the arena capacity fixed;
+ * f16 planes. */
 int wrs_kv_create(wrs_attn_ctx *ctx, size_t n_layers, size_t n_slots, size_t n_heads,
                   size_t max_ctx, size_t n_audio_max, wrs_kv **out);
+/* The same with the plane element type: WRS_F16 or WRS_F32 (the reference
+ * cache's Vec<f32>, decoder.rs:131-157). */
+int wrs_kv_create_dtype(wrs_attn_ctx *ctx, size_t n_layers, size_t n_slots, size_t n_heads,
+                        size_t max_ctx, size_t n_audio_max, int dtype, wrs_kv **out);
+/* Plane element type of an arena (WRS_F16 or WRS_F32). No reference
+ * counterpart: the reference cache has one type. */
+int wrs_kv_dtype(wrs_kv *kv, int *dtype);
 void wrs_kv_destroy(wrs_kv *kv);
 /* DecoderKvCache::clear (decoder.rs:162-176): every slot length to 0. */
 int wrs_kv_clear(wrs_kv *kv);
@@ -188,13 +207,14 @@ int wrs_kv_append(wrs_kv *kv, size_t layer, size_t slot, const float *k_rows,
                   const float *v_rows, size_t n, int src_on_host);
 int wrs_kv_advance(wrs_kv *kv, size_t slot, size_t n);
 /* Store of precompute_cross_attn (decoder.rs:423-447): f32 [n_audio][d_model]
- * K and V of one layer, converted to f16 head planes. */
+ * K and V of one layer, into the head planes (converted to f16, or copied). */
 int wrs_kv_set_cross(wrs_kv *kv, size_t layer, const float *k, const float *v, size_t n_audio,
                      int src_on_host);
 /* n_audio of one layer's stored cross K/V (DecoderKvCache keeps cross K/V per
  * layer, decoder.rs:136-139); 0 after wrs_kv_invalidate_cross. */
 int wrs_kv_cross_len(wrs_kv *kv, size_t layer, size_t *n_audio);
-/* Raw device pointers of the arena planes (for tests and fused callers). */
+/* Raw device pointers of the arena planes (for tests and fused callers);
+ * elements are of the arena's dtype, the slot stride in elements. */
 int wrs_kv_self_planes(wrs_kv *kv, void **k, void **v, size_t *slot_stride_elems);
 int wrs_kv_cross_planes(wrs_kv *kv, void **k, void **v);
 

@@ -124,6 +124,11 @@ pub mod ffi {
         // device KV arena: DecoderKvCache, decoder.rs:131-264
         pub fn wrs_kv_create(ctx: *mut WrsCtx, n_layers: usize, n_slots: usize, n_heads: usize,
             max_ctx: usize, n_audio_max: usize, out: *mut *mut WrsKv) -> c_int;
+        // the same with the plane element type (WRS_F16 or WRS_F32)
+        pub fn wrs_kv_create_dtype(ctx: *mut WrsCtx, n_layers: usize, n_slots: usize,
+            n_heads: usize, max_ctx: usize, n_audio_max: usize, dtype: c_int,
+            out: *mut *mut WrsKv) -> c_int;
+        pub fn wrs_kv_dtype(kv: *mut WrsKv, dtype: *mut c_int) -> c_int;
         pub fn wrs_kv_destroy(kv: *mut WrsKv);
         pub fn wrs_kv_clear(kv: *mut WrsKv) -> c_int;
         pub fn wrs_kv_clear_slot(kv: *mut WrsKv, slot: usize) -> c_int;
@@ -316,6 +321,18 @@ impl<'c> KvArena<'c> {
         let mut kv = std::ptr::null_mut();
         ctx.check(unsafe {
             wrs_kv_create(ctx.raw(), n_layers, n_slots, n_heads, max_ctx, n_audio_max, &mut kv)
+        });
+        KvArena { ctx, kv }
+    }
+
+    /// The same with f32 planes (`ffi::WRS_F32`): the reference cache's own
+    /// values, attention with the reference's arithmetic.
+    pub fn new_with_dtype(ctx: &'c AttnCtx, n_layers: usize, n_slots: usize, n_heads: usize,
+                          max_ctx: usize, n_audio_max: usize, dtype: c_int) -> Self {
+        let mut kv = std::ptr::null_mut();
+        ctx.check(unsafe {
+            wrs_kv_create_dtype(ctx.raw(), n_layers, n_slots, n_heads, max_ctx, n_audio_max,
+                                dtype, &mut kv)
         });
         KvArena { ctx, kv }
     }

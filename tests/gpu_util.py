@@ -32,6 +32,14 @@ def read_f16(ptr: int, offset_elems: int, n: int) -> np.ndarray:
     return out.astype(np.float32)
 
 
+def read_f32(ptr: int, offset_elems: int, n: int) -> np.ndarray:
+    """Copy n f32 values at device address ptr + 4*offset to host."""
+    out = np.empty(n, np.float32)
+    rc = hip().hipMemcpy(out.ctypes.data, ptr + 4 * offset_elems, 4 * n, 2)
+    assert rc == 0, f"hipMemcpy failed: {rc}"
+    return out
+
+
 def dev(x: np.ndarray, dtype=torch.float32) -> torch.Tensor:
     """Host float32 array (values exact in dtype) -> contiguous device tensor."""
     return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()

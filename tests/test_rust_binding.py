@@ -14,7 +14,8 @@ LIB_RS = CRATE / "src" / "lib.rs"
 
 # C type (whitespace-normalized) -> the Rust type that binds it
 C_TO_RUST = {
-    "int": "c_int", "void": "()", "size_t": "usize", "int64_t": "i64", "float": "f32",
+    "int": "c_int", "int *": "*mut c_int", "void": "()", "size_t": "usize", "int64_t": "i64",
+    "float": "f32",
     "const float *": "*const f32", "float *": "*mut f32",
     "const void *": "*const c_void", "void *": "*mut c_void", "void **": "*mut *mut c_void",
     "const char *": "*const c_char",

@@ -321,17 +321,28 @@ def _span(t) -> int:
 class KvArena:
     """Device KV cache (``wrs_kv``), methods named after DecoderKvCache."""
 
-    def __init__(self, n_layers, n_slots, n_heads, max_ctx, n_audio_max, ctx=None):
+    def __init__(self, n_layers, n_slots, n_heads, max_ctx, n_audio_max, ctx=None,
+                 dtype=WRS_F16):
+        """dtype WRS_F16 (default) or WRS_F32: the plane element type (WRS_F32
+        keeps the reference cache's f32 values and runs its arithmetic)."""
         self.ctx = ctx or default_context()
         self._lib = self.ctx._lib
         h = ctypes.c_void_p()
-        self.ctx.check(self._lib.wrs_kv_create(self.ctx.handle, n_layers, n_slots, n_heads,
-                                               max_ctx, n_audio_max, ctypes.byref(h)),
+        self.ctx.check(self._lib.wrs_kv_create_dtype(self.ctx.handle, n_layers, n_slots,
+                                                     n_heads, max_ctx, n_audio_max, dtype,
+                                                     ctypes.byref(h)),
                        "wrs_kv_create")
         self.handle = h
+        self.dtype = dtype
         self.n_layers, self.n_slots, self.n_heads = n_layers, n_slots, n_heads
         self.max_ctx, self.n_audio_max = max_ctx, n_audio_max
         self.d_model = n_heads * 64
+
+    def plane_dtype(self) -> int:
+        """Plane element type as the library reports it (WRS_F16 or WRS_F32)."""
+        d = ctypes.c_int()
+        self._c(self._lib.wrs_kv_dtype(self.handle, ctypes.byref(d)), "dtype")
+        return d.value
 
     def close(self):
         if getattr(self, "handle", None):
@@ -462,8 +473,8 @@ class KvArena:
 
     def set_cross_proj(self, enc, w_k, w_v, b_v=None):
         """precompute_cross_attn (crates/whisper/src/decoder.rs:423-447) into the
-        arena: per layer K = enc w_k^T, V = enc w_v^T + b_v, stored as f16
-        planes. ``enc`` [n_audio][d_model] float32/float16, ``w_k``/``w_v``
+        arena: per layer K = enc w_k^T, V = enc w_v^T + b_v, stored in the
+        arena's planes (rounded to f16, or as computed for f32 arenas). ``enc`` [n_audio][d_model] float32/float16, ``w_k``/``w_v``
         lists of [d_model][d_model] float16 tensors, ``b_v`` list of float32."""
         n = len(w_k)
         assert n == len(w_v) and (b_v is None or len(b_v) == n)

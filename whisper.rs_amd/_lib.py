@@ -76,6 +76,8 @@ _SIGNATURES = {
     "wrs_attn_prefill": (_int, [_vp, _int, _vp, _LP, _int, _vp, _LP, _vp, _LP, _vp, _LP, _sz, _sz,
                                 _sz, _sz, _sz, _int, _sz]),
     "wrs_kv_create": (_int, [_vp, _sz, _sz, _sz, _sz, _sz, ctypes.POINTER(_vp)]),
+    "wrs_kv_create_dtype": (_int, [_vp, _sz, _sz, _sz, _sz, _sz, _int, ctypes.POINTER(_vp)]),
+    "wrs_kv_dtype": (_int, [_vp, ctypes.POINTER(_int)]),
     "wrs_kv_destroy": (None, [_vp]),
     "wrs_kv_clear": (_int, [_vp]),
     "wrs_kv_clear_slot": (_int, [_vp, _sz]),

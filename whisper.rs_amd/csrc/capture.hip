@@ -35,6 +35,8 @@
 //   those come from its own f32 score sums, whose order differs from this
 //   kernel's exact-product sums, so weights agree with the two-pass ones to
 //   ~1e-6 relative rather than bit for bit.
+//
+// capture_cross_f32: the same weights over f32 cross planes, scalar.
 #include "wrs_internal.hpp"
 
 namespace wrs {
@@ -248,6 +250,63 @@ __global__ __launch_bounds__(kThreads) void capture_cross_f16(CaptureArgs a, int
   }
 }
 
+// Capture over f32 cross planes (the f32 arena), decoder.rs:814-825 as
+// written: one workgroup per (query row, pair); f32 scores dot * scale go into
+// the output row, then the row's max, exp, sum and reciprocal multiply
+// (softmax.rs:1-23) run over it in place. Each thread revisits only the keys
+// it scored, so only the reductions synchronize. No scratch.
+__device__ inline float block_reduce_f32(float x, float* sh, bool is_max) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float y = __shfl_xor(x, o);
+    x = is_max ? fmaxf(x, y) : x + y;
+  }
+  __syncthreads();  // the previous reduction's readers are done with sh
+  if (lane == 0) sh[wave] = x;
+  __syncthreads();
+  float r = sh[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = is_max ? fmaxf(r, sh[w]) : r + sh[w];
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void capture_cross_f32(CaptureArgs a) {
+  __shared__ float qsh[64];
+  __shared__ float sh[kWaves];
+  const int row = blockIdx.x, pair = blockIdx.y, tid = threadIdx.x;
+  const int head = a.head[pair];
+  const int n_audio = a.n_audio;
+  if (tid < 64) qsh[tid] = a.q[static_cast<int64_t>(row) * a.q_rs + head * 64 + tid];
+  __syncthreads();
+  float* dst = a.out + (static_cast<int64_t>(a.row_offset + row) * a.n_selected + a.slot[pair]) *
+                           static_cast<int64_t>(n_audio);
+  const float* kp = a.k32 + head * a.kv_hs;
+  float mx = -INFINITY;
+  for (int j = tid; j < n_audio; j += kThreads) {
+    const f32x4* kr = reinterpret_cast<const f32x4*>(kp + static_cast<int64_t>(j) * 64);
+    float dot = 0.0f;
+#pragma unroll
+    for (int d4 = 0; d4 < 16; ++d4) {
+      const f32x4 kv = kr[d4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dot = __builtin_fmaf(qsh[4 * d4 + e], kv[e], dot);
+    }
+    const float sc = dot * a.scale;
+    dst[j] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = block_reduce_f32(mx, sh, true);
+  float sum = 0.0f;
+  for (int j = tid; j < n_audio; j += kThreads) {
+    const float p = expf(dst[j] - mx);
+    dst[j] = p;
+    sum += p;
+  }
+  const float inv = 1.0f / block_reduce_f32(sum, sh, false);
+  for (int j = tid; j < n_audio; j += kThreads) dst[j] *= inv;
+}
+
 }  // namespace
 
 size_t capture_part_floats(int n_pairs, int n_tokens, int n_audio) {
@@ -274,6 +333,13 @@ hipError_t launch_capture_cross_f16(const CaptureArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(capture_cross_f16<1>, grid, dim3(kThreads), 0, s, a, n_blocks, n_chunks, n_xcd);
+  return hipGetLastError();
+}
+
+hipError_t launch_capture_cross_f32(const CaptureArgs& a, hipStream_t s) {
+  if (a.n_tokens <= 0 || a.n_pairs <= 0 || a.n_audio <= 0) return hipSuccess;
+  if (a.n_pairs > kMaxCapturePairs) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(capture_cross_f32, dim3(a.n_tokens, a.n_pairs), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -39,7 +39,8 @@
 // decode_exact_f32: the reference's own decode arithmetic on f32 K/V for the
 //   host-slice entry points: full score row, max, exp, sum, reciprocal
 //   multiply (softmax.rs:1-23), weights below 1e-7 skipped (attention.rs:366,
-//   decoder.rs:884). Row i of a call sees keys [0, row_limit0 + i).
+//   decoder.rs:884). Rows come in groups that share a K/V base; row i of
+//   group g sees keys [0, glen[g] + i * limit_step).
 #include "wrs_internal.hpp"
 
 namespace wrs {
@@ -426,11 +427,13 @@ __global__ __launch_bounds__(kThreads) void decode_exact_f32(ExactArgs a) {
   for (int d = tid; d < dh; d += kThreads) qsh[d] = q[d];
   __syncthreads();
 
-  const int L = a.row_limit0 + row;
+  const int g = row / a.rows_per_group;
+  const int L = a.glen[g] + (row - g * a.rows_per_group) * a.limit_step;
+  const int64_t kv0 = a.goff[g] + h * a.kv_hs;
   float* sc = a.scores + (static_cast<int64_t>(row) * a.n_heads + h) * a.scores_stride;
   float lmax = -INFINITY;
   for (int j = tid; j < L; j += kThreads) {
-    const float* kr = a.k + static_cast<int64_t>(j) * a.kv_rs + h * dh;
+    const float* kr = a.k + kv0 + static_cast<int64_t>(j) * a.kv_rs;
     float dot = 0.f;
     for (int d = 0; d < dh; ++d) dot = __builtin_fmaf(qsh[d], kr[d], dot);
     const float s = dot * a.scale;
@@ -456,7 +459,7 @@ __global__ __launch_bounds__(kThreads) void decode_exact_f32(ExactArgs a) {
       for (int j = qq; j < L; j += 4) {
         const float w = sc[j] * inv;
         if (w < 1e-7f) continue;
-        acc = __builtin_fmaf(w, a.v[static_cast<int64_t>(j) * a.kv_rs + h * dh + d], acc);
+        acc = __builtin_fmaf(w, a.v[kv0 + static_cast<int64_t>(j) * a.kv_rs + d], acc);
       }
     }
     accs[qq][dl] = acc;
@@ -595,6 +598,10 @@ hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s) {
 
 hipError_t launch_decode_exact_f32(const ExactArgs& a, hipStream_t s) {
   if (a.n_rows <= 0 || a.n_heads <= 0) return hipSuccess;
+  if (a.rows_per_group <= 0 || a.n_groups <= 0 || a.n_groups > kMaxExactGroups ||
+      static_cast<int64_t>(a.n_groups) * a.rows_per_group < a.n_rows || a.n_rows > 65535 ||
+      a.d_head <= 0 || a.d_head > 128)
+    return hipErrorInvalidValue;
   const dim3 grid(a.n_heads, a.n_rows), block(kThreads);
   hipLaunchKernelGGL(decode_exact_f32, grid, block, 0, s, a);
   return hipGetLastError();

@@ -1,10 +1,11 @@
 // K3: device KV arena kernels (the storage side of
 // crates/whisper/src/decoder.rs:131-264 DecoderKvCache).
 //
-// The arena keeps f16 planes of [ctx][64] per (layer, slot, head) for
-// self-attention and per (layer, head) for cross-attention. These kernels
-// convert the decoder's f32 projection rows into that layout and move rows
-// within / between planes.
+// The arena keeps planes of [ctx][64] per (layer, slot, head) for
+// self-attention and per (layer, head) for cross-attention, in f16 (default)
+// or f32. These kernels convert or copy the decoder's f32 projection rows into
+// that layout and move rows within / between planes; the row moves see an
+// f32 row as two f16-sized rows.
 #include "wrs_internal.hpp"
 
 namespace wrs {
@@ -31,6 +32,22 @@ __global__ void kv_write_rows(const float* src, int64_t src_rs, int n, int n_hea
   for (int e = 0; e < 8; ++e) x[e] = s[e];
   const f16x8 y = __builtin_convertvector(x, f16x8);
   *reinterpret_cast<f16x8*>(dst + h * dst_hs + static_cast<int64_t>(pos + i) * 64 + c * 8) = y;
+}
+
+// f32 planes: one thread per 4 values (row i, head h, 4-column group c). The
+// source rows need only 4-byte alignment; the plane rows are 256-byte aligned.
+__global__ void kv_write_rows_f32(const float* src, int64_t src_rs, int n, int n_heads,
+                                  float* dst, int64_t dst_hs, int pos) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(n) * n_heads * 16;
+  if (t >= total) return;
+  const int c = static_cast<int>(t & 15);
+  const int64_t ih = t >> 4;
+  const int h = static_cast<int>(ih % n_heads);
+  const int i = static_cast<int>(ih / n_heads);
+  const float* s = src + static_cast<int64_t>(i) * src_rs + h * 64 + c * 4;
+  const f32x4 x = {s[0], s[1], s[2], s[3]};
+  *reinterpret_cast<f32x4*>(dst + h * dst_hs + static_cast<int64_t>(pos + i) * 64 + c * 4) = x;
 }
 
 // One workgroup per plane. Rows move down in blocks of 32 rows (256 threads x
@@ -115,6 +132,17 @@ hipError_t launch_kv_write_rows(const float* src, int64_t src_rs, int n, int n_h
   const int64_t blocks = (total + 255) / 256;
   if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL(kv_write_rows, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src,
+                     src_rs, n, n_heads, dst, dst_hs, pos);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_write_rows_f32(const float* src, int64_t src_rs, int n, int n_heads,
+                                    float* dst, int64_t dst_hs, int pos, hipStream_t s) {
+  const int64_t total = static_cast<int64_t>(n) * n_heads * 16;
+  if (total <= 0) return hipSuccess;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(kv_write_rows_f32, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src,
                      src_rs, n, n_heads, dst, dst_hs, pos);
   return hipGetLastError();
 }

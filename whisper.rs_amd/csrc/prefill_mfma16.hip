@@ -123,14 +123,8 @@ __device__ inline f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
 // __builtin_amdgcn_permlane32_swap when both operands are the same value.)
 __device__ inline float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 
-// Four consecutive keys of one d column, from a row-major [key][d] LDS tile.
-__device__ inline u32x2 read_tr(const uint16_t* p) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_s16x4*)(reinterpret_cast<uintptr_t>(p)));
-  return __builtin_bit_cast(u32x2, v);
-}
-
-// The same from an LDS byte address, and 16 bytes at one.
+// Four consecutive keys of one d column of a row-major [key][d] LDS tile, from
+// an LDS byte address; and 16 bytes at one.
 __device__ inline u32x2 read_tr_at(uint32_t addr) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)addr);
   return __builtin_bit_cast(u32x2, v);

@@ -48,6 +48,8 @@ struct wrs_attn_ctx {
   size_t lin_x_bytes = 0;
   float* ln_x = nullptr;  // fused projections above the weight-stream size: normalized rows
   size_t ln_x_bytes = 0;
+  float* exact_scores = nullptr;  // f32 arena attention: full score rows
+  size_t exact_scores_bytes = 0;
   // Prefill schedule overrides (wrs_attn_set_schedule).
   int prefill_queries = 0;
   int f32_split = -1;
@@ -58,20 +60,32 @@ struct wrs_attn_ctx {
 
 struct wrs_kv {
   wrs_attn_ctx* ctx = nullptr;
+  int dtype = WRS_F16;  // element type of every plane: WRS_F16 or WRS_F32
   size_t n_layers = 0, n_slots = 0, n_heads = 0, max_ctx = 0, n_audio_max = 0;
-  uint16_t* k_self = nullptr;  // f16 [layer][slot][head][max_ctx][64]
-  uint16_t* v_self = nullptr;
-  uint16_t* k_cross = nullptr;  // f16 [layer][head][n_audio_max][64]
-  uint16_t* v_cross = nullptr;
+  void* k_self = nullptr;  // [layer][slot][head][max_ctx][64]
+  void* v_self = nullptr;
+  void* k_cross = nullptr;  // [layer][head][n_audio_max][64]
+  void* v_cross = nullptr;
   std::vector<size_t> len;        // per slot: rows stored (reference t_past)
   std::vector<size_t> cross_len;  // per layer: n_audio of the stored cross K/V
 
+  bool f32() const { return dtype == WRS_F32; }
+  size_t esize() const { return f32() ? 4 : 2; }
   size_t d_model() const { return n_heads * 64; }
   size_t plane() const { return max_ctx * 64; }
   size_t self_off(size_t layer, size_t slot) const {
     return ((layer * n_slots + slot) * n_heads) * plane();
   }
   size_t cross_off(size_t layer) const { return layer * n_heads * n_audio_max * 64; }
+  // Element `off` of a plane set, typed. words() views any plane set as
+  // 16-bit words (an f32 row of 64 is two f16-sized rows), so the row moves
+  // of kv_slide / kv_copy_planes serve both element types.
+  static uint16_t* u16(void* p, size_t off = 0) { return static_cast<uint16_t*>(p) + off; }
+  static float* f32p(void* p, size_t off = 0) { return static_cast<float*>(p) + off; }
+  _Float16* words(void* p, size_t off = 0) const {
+    return static_cast<_Float16*>(p) + off * (esize() / 2);
+  }
+  size_t word_scale() const { return esize() / 2; }
 };
 
 namespace {
@@ -182,12 +196,17 @@ int run_exact(wrs_attn_ctx* c, const float* q, size_t q_floats, const float* k, 
   a.v = dv;
   a.o = dout;
   a.q_rs = d_model;
-  a.kv_rs = d_model;
   a.o_rs = d_model;
+  a.kv_rs = d_model;
+  a.kv_hs = d_head;
   a.n_rows = n_rows;
   a.n_heads = n_heads;
   a.d_head = d_head;
-  a.row_limit0 = row_limit0;
+  a.rows_per_group = n_rows;
+  a.n_groups = 1;
+  a.limit_step = 1;
+  a.goff[0] = 0;
+  a.glen[0] = row_limit0;
   a.scale = 1.0f / std::sqrt(static_cast<float>(d_head));
   a.scores = ds;
   a.scores_stride = static_cast<int64_t>(std::max<size_t>(max_keys, 1));
@@ -455,6 +474,7 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
   if (c->cap_part) (void)hipFree(c->cap_part);
   if (c->lin_x) (void)hipFree(c->lin_x);
   if (c->ln_x) (void)hipFree(c->ln_x);
+  if (c->exact_scores) (void)hipFree(c->exact_scores);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   noalloc_release(c);  // the stream is drained: no call uses the slot any more
   delete c;
@@ -708,18 +728,91 @@ int wrs_attn_prefill(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layo
 
 // ---------------------------------------------------------------- KV arena
 
-int wrs_kv_create(wrs_attn_ctx* c, size_t n_layers, size_t n_slots, size_t n_heads,
-                  size_t max_ctx, size_t n_audio_max, wrs_kv** out) {
+}  // extern "C"
+
+namespace {
+
+// Rows [pos, pos + n) of every head plane of one plane set (element `off`
+// on), from n f32 rows of d_model: converted to f16, or copied for f32 arenas.
+int write_rows(wrs_attn_ctx* c, wrs_kv* kv, const float* src, int64_t src_rs, size_t n,
+               void* base, size_t off, int64_t plane, size_t pos) {
+  const int nh = static_cast<int>(kv->n_heads);
+  if (kv->f32())
+    WRS_HIP(c, wrs::launch_kv_write_rows_f32(src, src_rs, static_cast<int>(n), nh,
+                                             wrs_kv::f32p(base, off), plane,
+                                             static_cast<int>(pos), c->stream));
+  else
+    WRS_HIP(c, wrs::launch_kv_write_rows(src, src_rs, static_cast<int>(n), nh,
+                                         static_cast<_Float16*>(base) + off, plane,
+                                         static_cast<int>(pos), c->stream));
+  return WRS_OK;
+}
+
+// Attention over f32 arena planes on the exact decode kernel (the reference's
+// own single-token and cached-prompt arithmetic): n_rows query rows of d_model
+// in groups of rows_per_group that share the plane set at element goff[g];
+// row i of group g sees glen[g] + i * limit_step keys. At most
+// kMaxExactGroups groups and 65535 rows per call.
+int exact_arena(wrs_attn_ctx* c, wrs_kv* kv, const float* q, float* out, void* kbase,
+                void* vbase, int64_t kv_hs, const std::vector<int64_t>& goff,
+                const std::vector<int>& glen, int rows_per_group, int limit_step, int n_rows) {
+  if (n_rows <= 0) return WRS_OK;
+  const size_t groups = goff.size();
+  int max_len = 1;
+  for (size_t g = 0; g < groups; ++g)
+    max_len = std::max(max_len, glen[g] + (rows_per_group - 1) * limit_step);
+  const size_t bytes =
+      static_cast<size_t>(n_rows) * kv->n_heads * static_cast<size_t>(max_len) * sizeof(float);
+  int rc = grow(c, reinterpret_cast<void**>(&c->exact_scores), &c->exact_scores_bytes, bytes,
+                false);
+  if (rc) return rc;
+  wrs::ExactArgs a{};
+  a.q = q;
+  a.k = static_cast<const float*>(kbase);
+  a.v = static_cast<const float*>(vbase);
+  a.o = out;
+  a.q_rs = static_cast<int64_t>(kv->d_model());
+  a.o_rs = a.q_rs;
+  a.kv_rs = 64;
+  a.kv_hs = kv_hs;
+  a.n_rows = n_rows;
+  a.n_heads = static_cast<int>(kv->n_heads);
+  a.d_head = 64;
+  a.rows_per_group = rows_per_group;
+  a.n_groups = static_cast<int>(groups);
+  a.limit_step = limit_step;
+  a.scale = 0.125f;  // 1/sqrt(64) (attention.rs:255, decoder.rs:857)
+  a.scores = c->exact_scores;
+  a.scores_stride = max_len;
+  for (size_t g = 0; g < groups; ++g) {
+    a.goff[g] = goff[g];
+    a.glen[g] = glen[g];
+  }
+  WRS_HIP(c, wrs::launch_decode_exact_f32(a, c->stream));
+  return WRS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wrs_kv_create_dtype(wrs_attn_ctx* c, size_t n_layers, size_t n_slots, size_t n_heads,
+                        size_t max_ctx, size_t n_audio_max, int dtype, wrs_kv** out) {
   if (!c || !out) return WRS_EINVAL;
   *out = nullptr;
   if (n_layers == 0 || n_heads == 0 || max_ctx == 0 || !fits_int(max_ctx) ||
       !fits_int(n_audio_max) || !fits_int(n_slots))
+    return fail(c, WRS_EINVAL, "wrs_kv_create: bad geometry");
+  if (dtype != WRS_F16 && dtype != WRS_F32)
+    return fail(c, WRS_EINVAL, "wrs_kv_create: arena dtype must be WRS_F16 or WRS_F32");
+  if (dtype == WRS_F32 && !fits_int(2 * max_ctx))  // row moves count f16-sized rows
     return fail(c, WRS_EINVAL, "wrs_kv_create: bad geometry");
   std::lock_guard<std::mutex> lk(c->mu);
   DeviceGuard g(c->device);
   auto* kv = new (std::nothrow) wrs_kv();
   if (!kv) return WRS_ENOMEM;
   kv->ctx = c;
+  kv->dtype = dtype;
   kv->n_layers = n_layers;
   kv->n_slots = n_slots;
   kv->n_heads = n_heads;
@@ -727,8 +820,8 @@ int wrs_kv_create(wrs_attn_ctx* c, size_t n_layers, size_t n_slots, size_t n_hea
   kv->n_audio_max = n_audio_max;
   kv->len.assign(n_slots, 0);
   kv->cross_len.assign(n_layers, 0);
-  const size_t self_bytes = n_layers * n_slots * n_heads * max_ctx * 64 * 2;
-  const size_t cross_bytes = n_layers * n_heads * n_audio_max * 64 * 2;
+  const size_t self_bytes = n_layers * n_slots * n_heads * max_ctx * 64 * kv->esize();
+  const size_t cross_bytes = n_layers * n_heads * n_audio_max * 64 * kv->esize();
   bool ok = true;
   if (self_bytes) {
     ok = ok && hipMalloc(&kv->k_self, self_bytes) == hipSuccess;
@@ -745,6 +838,17 @@ int wrs_kv_create(wrs_attn_ctx* c, size_t n_layers, size_t n_slots, size_t n_hea
     return fail(c, WRS_ENOMEM, "wrs_kv_create: hipMalloc failed");
   }
   *out = kv;
+  return WRS_OK;
+}
+
+int wrs_kv_create(wrs_attn_ctx* c, size_t n_layers, size_t n_slots, size_t n_heads,
+                  size_t max_ctx, size_t n_audio_max, wrs_kv** out) {
+  return wrs_kv_create_dtype(c, n_layers, n_slots, n_heads, max_ctx, n_audio_max, WRS_F16, out);
+}
+
+int wrs_kv_dtype(wrs_kv* kv, int* dtype) {
+  if (!kv || !dtype) return WRS_EINVAL;
+  *dtype = kv->dtype;
   return WRS_OK;
 }
 
@@ -788,9 +892,9 @@ int wrs_kv_ensure_slots(wrs_kv* kv, size_t n_slots) {
   if (n_slots <= kv->n_slots) return WRS_OK;
   if (!fits_int(n_slots)) return fail(c, WRS_EINVAL, "n_slots exceeds 2^31");
   DeviceGuard g(c->device);
-  const size_t slot_bytes = kv->n_heads * kv->plane() * 2;
+  const size_t slot_bytes = kv->n_heads * kv->plane() * kv->esize();
   const size_t bytes = kv->n_layers * n_slots * slot_bytes;
-  uint16_t *nk = nullptr, *nv = nullptr;
+  void *nk = nullptr, *nv = nullptr;
   if (hipMalloc(&nk, bytes) != hipSuccess || hipMalloc(&nv, bytes) != hipSuccess) {
     if (nk) (void)hipFree(nk);
     return fail(c, WRS_ENOMEM, "wrs_kv_ensure_slots: hipMalloc failed");
@@ -819,16 +923,19 @@ int wrs_kv_copy_slot(wrs_kv* kv, size_t dst, size_t src) {
   if (dst >= kv->n_slots || src >= kv->n_slots) return fail(c, WRS_ERANGE, "slot out of range");
   if (dst == src) return WRS_OK;
   DeviceGuard g(c->device);
-  const int64_t layer_stride = static_cast<int64_t>(kv->n_slots * kv->n_heads * kv->plane());
-  const int64_t plane = static_cast<int64_t>(kv->plane());
-  const int n = static_cast<int>(kv->len[src]);
-  auto* ks = reinterpret_cast<_Float16*>(kv->k_self);
-  auto* vs = reinterpret_cast<_Float16*>(kv->v_self);
-  WRS_HIP(c, wrs::launch_kv_copy_planes(ks + kv->self_off(0, src), ks + kv->self_off(0, dst),
-                                        layer_stride, plane, static_cast<int>(kv->n_layers),
+  // Strides and row counts in f16-sized rows (twice the rows for f32 planes).
+  const size_t w = kv->word_scale();
+  const int64_t layer_stride =
+      static_cast<int64_t>(kv->n_slots * kv->n_heads * kv->plane() * w);
+  const int64_t plane = static_cast<int64_t>(kv->plane() * w);
+  const int n = static_cast<int>(kv->len[src] * w);
+  WRS_HIP(c, wrs::launch_kv_copy_planes(kv->words(kv->k_self, kv->self_off(0, src)),
+                                        kv->words(kv->k_self, kv->self_off(0, dst)), layer_stride,
+                                        plane, static_cast<int>(kv->n_layers),
                                         static_cast<int>(kv->n_heads), n, c->stream));
-  WRS_HIP(c, wrs::launch_kv_copy_planes(vs + kv->self_off(0, src), vs + kv->self_off(0, dst),
-                                        layer_stride, plane, static_cast<int>(kv->n_layers),
+  WRS_HIP(c, wrs::launch_kv_copy_planes(kv->words(kv->v_self, kv->self_off(0, src)),
+                                        kv->words(kv->v_self, kv->self_off(0, dst)), layer_stride,
+                                        plane, static_cast<int>(kv->n_layers),
                                         static_cast<int>(kv->n_heads), n, c->stream));
   kv->len[dst] = kv->len[src];
   return WRS_OK;
@@ -861,16 +968,16 @@ int wrs_kv_slide_to_fit(wrs_kv* kv, size_t slot, size_t n_new, size_t max_ctx, s
   if (t_past + n_new > max_ctx) {  // decoder.rs:250-261
     const size_t drop = std::min(t_past + n_new - max_ctx, t_past);
     DeviceGuard g(c->device);
-    const int64_t layer_stride = static_cast<int64_t>(kv->n_slots * kv->n_heads * kv->plane());
-    const int64_t plane = static_cast<int64_t>(kv->plane());
-    auto* ks = reinterpret_cast<_Float16*>(kv->k_self);
-    auto* vs = reinterpret_cast<_Float16*>(kv->v_self);
-    WRS_HIP(c, wrs::launch_kv_slide(ks + kv->self_off(0, slot), layer_stride, plane,
-                                    static_cast<int>(kv->n_layers), static_cast<int>(kv->n_heads),
-                                    static_cast<int>(t_past), static_cast<int>(drop), c->stream));
-    WRS_HIP(c, wrs::launch_kv_slide(vs + kv->self_off(0, slot), layer_stride, plane,
-                                    static_cast<int>(kv->n_layers), static_cast<int>(kv->n_heads),
-                                    static_cast<int>(t_past), static_cast<int>(drop), c->stream));
+    // In f16-sized rows: an f32 row moves as two.
+    const size_t w = kv->word_scale();
+    const int64_t layer_stride =
+        static_cast<int64_t>(kv->n_slots * kv->n_heads * kv->plane() * w);
+    const int64_t plane = static_cast<int64_t>(kv->plane() * w);
+    for (void* base : {kv->k_self, kv->v_self})
+      WRS_HIP(c, wrs::launch_kv_slide(kv->words(base, kv->self_off(0, slot)), layer_stride, plane,
+                                      static_cast<int>(kv->n_layers),
+                                      static_cast<int>(kv->n_heads), static_cast<int>(t_past * w),
+                                      static_cast<int>(drop * w), c->stream));
     t_past -= drop;
     kv->len[slot] = t_past;
   }
@@ -901,12 +1008,11 @@ int wrs_kv_append(wrs_kv* kv, size_t layer, size_t slot, const float* k_rows,
   if (rc) return rc;
   const int64_t dm = static_cast<int64_t>(kv->d_model());
   const int64_t plane = static_cast<int64_t>(kv->plane());
-  auto* ks = reinterpret_cast<_Float16*>(kv->k_self) + kv->self_off(layer, slot);
-  auto* vs = reinterpret_cast<_Float16*>(kv->v_self) + kv->self_off(layer, slot);
-  WRS_HIP(c, wrs::launch_kv_write_rows(dk, dm, static_cast<int>(n), static_cast<int>(kv->n_heads),
-                                       ks, plane, static_cast<int>(pos), c->stream));
-  WRS_HIP(c, wrs::launch_kv_write_rows(dv, dm, static_cast<int>(n), static_cast<int>(kv->n_heads),
-                                       vs, plane, static_cast<int>(pos), c->stream));
+  const size_t off = kv->self_off(layer, slot);
+  rc = write_rows(c, kv, dk, dm, n, kv->k_self, off, plane, pos);
+  if (rc) return rc;
+  rc = write_rows(c, kv, dv, dm, n, kv->v_self, off, plane, pos);
+  if (rc) return rc;
   if (src_on_host) WRS_HIP(c, hipStreamSynchronize(c->stream));
   return WRS_OK;
 }
@@ -942,12 +1048,10 @@ int wrs_kv_set_cross(wrs_kv* kv, size_t layer, const float* k, const float* v, s
     if (rc) return rc;
     const int64_t dm = static_cast<int64_t>(kv->d_model());
     const int64_t plane = static_cast<int64_t>(kv->n_audio_max * 64);
-    auto* kc = reinterpret_cast<_Float16*>(kv->k_cross) + kv->cross_off(layer);
-    auto* vc = reinterpret_cast<_Float16*>(kv->v_cross) + kv->cross_off(layer);
-    WRS_HIP(c, wrs::launch_kv_write_rows(dk, dm, static_cast<int>(n_audio),
-                                         static_cast<int>(kv->n_heads), kc, plane, 0, c->stream));
-    WRS_HIP(c, wrs::launch_kv_write_rows(dv, dm, static_cast<int>(n_audio),
-                                         static_cast<int>(kv->n_heads), vc, plane, 0, c->stream));
+    rc = write_rows(c, kv, dk, dm, n_audio, kv->k_cross, kv->cross_off(layer), plane, 0);
+    if (rc) return rc;
+    rc = write_rows(c, kv, dv, dm, n_audio, kv->v_cross, kv->cross_off(layer), plane, 0);
+    if (rc) return rc;
     if (src_on_host) WRS_HIP(c, hipStreamSynchronize(c->stream));
   }
   kv->cross_len[layer] = n_audio;
@@ -1000,9 +1104,13 @@ int wrs_attn_decode_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const size_t
       goff[i] = static_cast<int64_t>(kv->self_off(layer, s));
       lens[i] = static_cast<int>(kv->len[s] + 1);
     }
-    int rc = decode_impl(c, q + i0 * dm, dm, out + i0 * dm, dm, kv->k_self, kv->v_self,
-                         static_cast<int64_t>(kv->plane()), goff, lens, 1,
-                         static_cast<int>(kv->n_heads));
+    int rc = kv->f32()
+                 ? exact_arena(c, kv, q + i0 * dm, out + i0 * dm, kv->k_self, kv->v_self,
+                               static_cast<int64_t>(kv->plane()), goff, lens, 1, 0,
+                               static_cast<int>(m))
+                 : decode_impl(c, q + i0 * dm, dm, out + i0 * dm, dm, wrs_kv::u16(kv->k_self),
+                               wrs_kv::u16(kv->v_self), static_cast<int64_t>(kv->plane()), goff,
+                               lens, 1, static_cast<int>(kv->n_heads));
     if (rc) return rc;
   }
   return WRS_OK;
@@ -1028,6 +1136,21 @@ int decode_cross_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
                                           static_cast<int>(dm), c->stream));
     return WRS_OK;
   }
+  if (kv->f32()) {
+    // f32 arena: every beam row on the exact kernel (attention.rs:246-434,
+    // the single-token path each beam's decoder call takes).
+    if (fixed) return fail(c, WRS_EUNSUPPORTED, "allocation-free decode needs an f16 arena");
+    constexpr size_t kRows = 4096;
+    for (size_t b0 = 0; b0 < n_beams; b0 += kRows) {
+      const int rows = static_cast<int>(std::min(kRows, n_beams - b0));
+      int rc = exact_arena(c, kv, q + b0 * dm, out + b0 * dm, kv->k_cross, kv->v_cross,
+                           static_cast<int64_t>(kv->n_audio_max * 64),
+                           {static_cast<int64_t>(kv->cross_off(layer))}, {static_cast<int>(L)},
+                           rows, 0, rows);
+      if (rc) return rc;
+    }
+    return WRS_OK;
+  }
   // All beams of the utterance share one read of the plane; beyond 8 beams the
   // rows go in further launches of up to 8 (which reuse the same scratch in
   // stream order).
@@ -1035,9 +1158,9 @@ int decode_cross_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q,
     const size_t rows = std::min<size_t>(wrs::kMaxRowsPerGroup, n_beams - b0);
     std::vector<int64_t> goff(1, static_cast<int64_t>(kv->cross_off(layer)));
     std::vector<int> lens(1, static_cast<int>(L));
-    int rc = decode_impl(c, q + b0 * dm, dm, out + b0 * dm, dm, kv->k_cross, kv->v_cross,
-                         static_cast<int64_t>(kv->n_audio_max * 64), goff, lens,
-                         static_cast<int>(rows), static_cast<int>(kv->n_heads), fixed);
+    int rc = decode_impl(c, q + b0 * dm, dm, out + b0 * dm, dm, wrs_kv::u16(kv->k_cross),
+                         wrs_kv::u16(kv->v_cross), static_cast<int64_t>(kv->n_audio_max * 64),
+                         goff, lens, static_cast<int>(rows), static_cast<int>(kv->n_heads), fixed);
     if (rc) return rc;
   }
   return WRS_OK;
@@ -1064,6 +1187,22 @@ int cross_rows_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, s
                                           static_cast<int>(dm), c->stream));
     return WRS_OK;
   }
+  if (kv->f32()) {
+    // f32 arena: the prompt rows as flash_attention_2 takes them
+    // (attention.rs:79-105): one row on the exact single-token kernel, more on
+    // the f32 prefill kernel. No row statistics on this path.
+    if (lse) return fail(c, WRS_EUNSUPPORTED, "row statistics need an f16 arena");
+    const int64_t plane = static_cast<int64_t>(kv->n_audio_max * 64);
+    if (n == 1)
+      return exact_arena(c, kv, q, out, kv->k_cross, kv->v_cross, plane,
+                         {static_cast<int64_t>(kv->cross_off(layer))}, {static_cast<int>(L)}, 1,
+                         0, 1);
+    const wrs_layout lq{0, 64, dm};
+    const wrs_layout lkv{0, plane, 64};
+    return prefill_impl(c, WRS_F32, q, lq, WRS_F32, wrs_kv::f32p(kv->k_cross, kv->cross_off(layer)),
+                        lkv, wrs_kv::f32p(kv->v_cross, kv->cross_off(layer)), lkv, out, lq, 1,
+                        kv->n_heads, n, L, 64, 0, 0);
+  }
   for (size_t r0 = 0; r0 < n;) {
     const size_t left = n - r0;
     const int rpg = static_cast<int>(std::min<size_t>(left, wrs::kMaxRowsPerGroup));
@@ -1073,8 +1212,9 @@ int cross_rows_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, s
             : 1;
     std::vector<int64_t> goff(groups, static_cast<int64_t>(kv->cross_off(layer)));
     std::vector<int> lens(groups, static_cast<int>(L));
-    int rc = decode_impl(c, q + r0 * dm, dm, out + r0 * dm, dm, kv->k_cross, kv->v_cross,
-                         static_cast<int64_t>(kv->n_audio_max * 64), goff, lens, rpg,
+    int rc = decode_impl(c, q + r0 * dm, dm, out + r0 * dm, dm, wrs_kv::u16(kv->k_cross),
+                         wrs_kv::u16(kv->v_cross), static_cast<int64_t>(kv->n_audio_max * 64),
+                         goff, lens, rpg,
                          static_cast<int>(kv->n_heads), nullptr, lse, static_cast<int>(n),
                          static_cast<int>(r0));
     if (rc) return rc;
@@ -1098,6 +1238,7 @@ int wrs_attn_decode_cross_noalloc(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, con
                                   size_t n_beams, float* out) {
   if (!c || !kv) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
+  if (kv->f32()) return fail(c, WRS_EUNSUPPORTED, "allocation-free decode needs an f16 arena");
   int rc = WRS_OK;
   unsigned char* fixed = noalloc_slot_ptr(c, &rc);
   if (!fixed) return rc;
@@ -1115,10 +1256,24 @@ int wrs_attn_prefill_self(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, size_t slot
   if (t_past + n_tokens > kv->max_ctx) return fail(c, WRS_ERANGE, "rows past max_ctx");
   DeviceGuard g(c->device);
   const int64_t dm = static_cast<int64_t>(kv->d_model());
+  if (kv->f32()) {
+    // f32 arena: mha_with_cache's multi-token path (decoder.rs:857-892) on the
+    // exact kernel; prompt row i sees t_past + 1 + i keys.
+    constexpr size_t kRows = 4096;
+    for (size_t r0 = 0; r0 < n_tokens; r0 += kRows) {
+      const int rows = static_cast<int>(std::min(kRows, n_tokens - r0));
+      int rc = exact_arena(c, kv, q + r0 * dm, out + r0 * dm, kv->k_self, kv->v_self,
+                           static_cast<int64_t>(kv->plane()),
+                           {static_cast<int64_t>(kv->self_off(layer, slot))},
+                           {static_cast<int>(t_past + 1 + r0)}, rows, 1, rows);
+      if (rc) return rc;
+    }
+    return WRS_OK;
+  }
   const wrs_layout lq{0, 64, dm};
   const wrs_layout lkv{0, static_cast<int64_t>(kv->plane()), 64};
-  const uint16_t* kb = kv->k_self + kv->self_off(layer, slot);
-  const uint16_t* vb = kv->v_self + kv->self_off(layer, slot);
+  const uint16_t* kb = wrs_kv::u16(kv->k_self, kv->self_off(layer, slot));
+  const uint16_t* vb = wrs_kv::u16(kv->v_self, kv->self_off(layer, slot));
   return prefill_impl(c, WRS_F32, q, lq, WRS_F16, kb, lkv, vb, lkv, out, lq, 1, kv->n_heads,
                       n_tokens, t_past + n_tokens, 64, 1, t_past);
 }
@@ -1171,7 +1326,6 @@ int capture_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, size
   DeviceGuard g(c->device);
   wrs::CaptureArgs a{};
   a.q = q;
-  a.k = reinterpret_cast<const _Float16*>(kv->k_cross + kv->cross_off(layer));
   a.out = out;
   a.q_rs = static_cast<int64_t>(kv->d_model());
   a.kv_hs = static_cast<int64_t>(kv->n_audio_max * 64);
@@ -1181,6 +1335,24 @@ int capture_impl(wrs_attn_ctx* c, wrs_kv* kv, size_t layer, const float* q, size
   a.row_offset = static_cast<int>(row_offset);
   a.scale_log2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) (decoder.rs:810) * log2(e)
   a.lse = lse;
+  if (kv->f32()) {
+    // f32 planes: scores and softmax as decoder.rs:814-825 computes them, one
+    // workgroup per (row, pair); row statistics are not used.
+    if (lse) return fail(c, WRS_EUNSUPPORTED, "row statistics need an f16 arena");
+    a.k32 = wrs_kv::f32p(kv->k_cross, kv->cross_off(layer));
+    a.scale = 0.125f;  // 1/sqrt(64) (decoder.rs:810)
+    for (size_t p0 = 0; p0 < n_pairs; p0 += wrs::kMaxCapturePairs) {
+      const size_t np = std::min<size_t>(wrs::kMaxCapturePairs, n_pairs - p0);
+      a.n_pairs = static_cast<int>(np);
+      for (size_t p = 0; p < np; ++p) {
+        a.slot[p] = static_cast<int>(slots[p0 + p]);
+        a.head[p] = static_cast<int>(heads[p0 + p]);
+      }
+      WRS_HIP(c, wrs::launch_capture_cross_f32(a, c->stream));
+    }
+    return WRS_OK;
+  }
+  a.k = reinterpret_cast<const _Float16*>(wrs_kv::u16(kv->k_cross, kv->cross_off(layer)));
   if (!lse) {  // two passes: chunk statistics in the context
     const size_t pb =
         wrs::capture_part_floats(static_cast<int>(std::min<size_t>(n_pairs, wrs::kMaxCapturePairs)),
@@ -1507,12 +1679,12 @@ int wrs_kv_set_cross_proj(wrs_kv* kv, int x_dtype, const void* enc, size_t enc_l
         const size_t l = l0 + i;
         a.w[2 * i] = static_cast<const _Float16*>(w_k[l]);
         a.bias[2 * i] = nullptr;
-        a.out[2 * i] = reinterpret_cast<_Float16*>(kv->k_cross) + kv->cross_off(l);
+        a.out[2 * i] = kv->words(kv->k_cross, kv->cross_off(l));
         a.w[2 * i + 1] = static_cast<const _Float16*>(w_v[l]);
         a.bias[2 * i + 1] = b_v ? b_v[l] : nullptr;
-        a.out[2 * i + 1] = reinterpret_cast<_Float16*>(kv->v_cross) + kv->cross_off(l);
+        a.out[2 * i + 1] = kv->words(kv->v_cross, kv->cross_off(l));
       }
-      WRS_HIP(c, wrs::launch_linear_f16w(a, wrs::kF16, c->stream));
+      WRS_HIP(c, wrs::launch_linear_f16w(a, kv->f32() ? wrs::kF32 : wrs::kF16, c->stream));
     }
   }
   for (size_t l = 0; l < kv->n_layers; ++l) kv->cross_len[l] = n_audio;

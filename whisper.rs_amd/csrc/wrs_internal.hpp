@@ -4,8 +4,8 @@
 //   activations  element (b, h, t, d) at base + b*bs + h*hs + t*rs + d
 //                (token-major [T][n_heads*d_head] rows of the reference are
 //                 hs = d_head, rs = d_model; BHSD is hs = T*d_head, rs = d_head)
-//   KV cache     f16, one [ctx][64] plane per (layer, slot, head) -- rows of
-//                one head are contiguous 128-byte lines.
+//   KV cache     f16 (or f32), one [ctx][64] plane per (layer, slot, head) --
+//                rows of one head are contiguous 128-byte (256-byte) lines.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -62,21 +62,28 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s);
 // exactly to f32, any d_head <= 128.
 hipError_t launch_prefill_f32(const PrefillArgs& a, DType q_dt, DType kv_dt, hipStream_t s);
 
-// Exact reference decode semantics for f32 host-slice calls
-// (attention.rs:246-434 single_token_mha_d64 and decoder.rs:835-892):
-// full score row, softmax with reciprocal multiply, weights < 1e-7 skipped.
-// Row i sees keys [0, row_limit0 + i) (row_limit0 = t_kv for single-token).
+// Exact reference decode semantics on f32 K/V (attention.rs:246-434
+// single_token_mha_d64 and decoder.rs:835-892): full score row, softmax with
+// reciprocal multiply, weights < 1e-7 skipped. Rows come in groups of
+// rows_per_group that share one K/V base (goff[g] elements past k and v);
+// row i of group g sees keys [0, glen[g] + i * limit_step). Host slices are
+// one group of token-major rows (kv_rs = d_model, kv_hs = d_head); the f32
+// arena passes [head][ctx][64] planes (kv_rs = 64, kv_hs = the plane).
+constexpr int kMaxExactGroups = 64;
 struct ExactArgs {
   const float* q;
   const float* k;
   const float* v;
   float* o;
-  int64_t q_rs, kv_rs, o_rs;  // row strides (d_model)
+  int64_t q_rs, o_rs;   // row strides of q and out (head h at h * d_head)
+  int64_t kv_rs, kv_hs;  // K/V: key row and head strides
   int n_rows, n_heads, d_head;
-  int row_limit0;
+  int rows_per_group, n_groups, limit_step;
   float scale;
   float* scores;  // scratch [n_rows][n_heads][scores_stride]
   int64_t scores_stride;
+  int64_t goff[kMaxExactGroups];
+  int glen[kMaxExactGroups];
 };
 hipError_t launch_decode_exact_f32(const ExactArgs& a, hipStream_t s);
 
@@ -131,6 +138,8 @@ constexpr int kMaxCapturePairs = 32;   // (slot, head) pairs per launch
 struct CaptureArgs {
   const float* q;     // row i, head h: q + i*q_rs + h*64
   const _Float16* k;  // plane of head h: k + h*kv_hs, key j at +j*64
+  const float* k32;   // the same for f32 planes (capture_cross_f32)
+  float scale;        // 1/sqrt(64), capture_cross_f32
   float* out;
   float* part;        // scratch: capture_part_floats(n_pairs, n_tokens, n_audio)
   int64_t q_rs, kv_hs;
@@ -145,6 +154,8 @@ struct CaptureArgs {
 };
 size_t capture_part_floats(int n_pairs, int n_tokens, int n_audio);
 hipError_t launch_capture_cross_f16(const CaptureArgs& a, hipStream_t s);
+// Over f32 planes (k32, scale; no part, no lse): one workgroup per (row, pair).
+hipError_t launch_capture_cross_f32(const CaptureArgs& a, hipStream_t s);
 
 // Projections with f16 weights (quant.rs:415-473 semantics):
 // out(t, r) = row_scale[t] * (W[r] . x'[t]) + bias[r] with W [n_out][n_in] f16
@@ -210,7 +221,11 @@ hipError_t launch_fill_zero_u32(unsigned* p, int64_t n, hipStream_t s);
 // dst + h*dst_hs + (pos + i)*64.
 hipError_t launch_kv_write_rows(const float* src, int64_t src_rs, int n, int n_heads,
                                 _Float16* dst, int64_t dst_hs, int pos, hipStream_t s);
-// Planes of one slot: plane (l, h) at base + l*layer_stride + h*plane_stride.
+// The same into f32 planes (a copy).
+hipError_t launch_kv_write_rows_f32(const float* src, int64_t src_rs, int n, int n_heads,
+                                    float* dst, int64_t dst_hs, int pos, hipStream_t s);
+// Planes of one slot: plane (l, h) at base + l*layer_stride + h*plane_stride,
+// in rows of 64 f16 (an f32 plane is passed as twice the rows and strides).
 // Move rows [drop, len) of every plane down to [0, len - drop).
 hipError_t launch_kv_slide(_Float16* base, int64_t layer_stride, int64_t plane_stride,
                            int n_layers, int n_heads, int len, int drop, hipStream_t s);
