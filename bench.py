@@ -735,6 +735,87 @@ def bench_host_slice(wrs, W, ctx, reps=20):
             "pcie_bytes_per_call": 4 * q.nbytes}
 
 
+# (t_q, t_kv) of the reference's attention microbenchmark, 6 heads of 64
+# (crates/tensor/tests/bench_flash_attention_tiled.rs:19-25): an encoder row of
+# 1500 frames, a 64-row cross-attention call, and a shape whose score matrix
+# outgrows the last-level cache.
+REFERENCE_SHAPES = ((1500, 1500), (64, 1500), (4096, 4096))
+
+
+def _reference_shape_inputs(t_q, t_kv, n_heads=6):
+    """f32 Q, K, V uniform in [-1, 1), seeded per shape (the microbenchmark's
+    value range; its own generator is xorshift32)."""
+    rng = np.random.default_rng(0x5EED0000 + 7919 * t_q + t_kv)
+    dm = 64 * n_heads
+    return tuple(rng.uniform(-1.0, 1.0, size=(t, dm)).astype(np.float32)
+                 for t in (t_q, t_kv, t_kv))
+
+
+def bench_reference_shapes(wrs, ctx, reps=20):
+    """flash_attention_2 at the reference microbenchmark's shapes, f32, no mask:
+    the host-slice drop-in (PCIe both ways, synchronous) and the same call on
+    device-resident tensors (the f32 prefill kernel), per shape."""
+    import torch
+    res = {}
+    H = 6
+    for t_q, t_kv in REFERENCE_SHAPES:
+        q, k, v = _reference_shape_inputs(t_q, t_kv, H)
+        dm = q.shape[1]
+        out = np.empty_like(q)
+        for _ in range(3):
+            wrs.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, out, ctx=ctx)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            wrs.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, out, ctx=ctx)
+        host_ms = (time.perf_counter() - t0) * 1e3 / reps
+        qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+        od = torch.empty_like(qd)
+        lq, lkv = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+        run = lambda: wrs.prefill(qd, kd, vd, od, batch=1, n_heads=H, t_q=t_q, t_kv=t_kv,
+                                  d_head=64, q_layout=lq, kv_layout=lkv, out_layout=lq, ctx=ctx)
+        for _ in range(20):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        e1.synchronize()
+        dev_ms = e0.elapsed_time(e1) / reps
+        gflop = 4.0 * H * t_q * t_kv * 64 / 1e9
+        res[f"{t_q}x{t_kv}"] = {
+            "host_slice_ms": round(host_ms, 4),
+            "host_slice_GFLOPs": round(gflop / host_ms * 1e3, 1),
+            "device_resident_ms": round(dev_ms, 4),
+            "device_resident_GFLOPs": round(gflop / dev_ms * 1e3, 1),
+            "pcie_bytes_per_call": 4 * (q.nbytes + k.nbytes + v.nbytes + out.nbytes)}
+        log(f"reference shape ({t_q}, {t_kv}) x {H} heads: host slices {host_ms:.3f} ms, "
+            f"device-resident {dev_ms * 1e3:.1f} us ({gflop / dev_ms:.1f} TFLOP/s)")
+        del qd, kd, vd, od
+    return res
+
+
+def cpu_baseline_reference_shapes(info):
+    """The oracle's tiled flash_attention_2 at the same shapes and inputs, best
+    of 9 on available_parallelism() threads (best of 3 at (4096, 4096))."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    n = info["threads"]
+    res = {}
+    for t_q, t_kv in REFERENCE_SHAPES:
+        q, k, v = (np.ascontiguousarray(x.reshape(-1)) for x in _reference_shape_inputs(t_q, t_kv))
+        dm = 384
+        out = np.zeros_like(q)
+        fn = lambda: orc.flash_attention_2(q, k, v, t_q, t_kv, 6, dm, False, out, n_threads=n)
+        fn()
+        t = time_best(fn, reps=3 if t_q * t_kv > 4_000_000 else REPS)
+        gflop = 4.0 * 6 * t_q * t_kv * 64 / 1e9
+        res[f"{t_q}x{t_kv}"] = {"ms": round(t * 1e3, 2), "GFLOPs": round(gflop / t, 1),
+                                "cores": n, "kind": "port"}
+    return res
+
+
 def copy_bandwidth():
     import torch
     n = 1 << 28  # 1 GiB of f32
@@ -1048,7 +1129,7 @@ def main():
     ap.add_argument("--rows-reps", type=int, default=50)
     ap.add_argument("--only", choices=["encoder", "encoder_base", "decode", "decode_self",
                                        "capture", "linear", "stream", "rows", "host_slice",
-                                       "traffic"],
+                                       "reference_shapes", "traffic"],
                     default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
@@ -1104,6 +1185,9 @@ def main():
         log(f"stream only: step {sms:.3f} ms, {sgbs:.1f} GB/s; vocabulary {vms * 1e3:.1f} us, "
             f"{vgbs:.1f} GB/s")
         return
+    if args.only == "reference_shapes":
+        bench_reference_shapes(wrs, ctx)
+        return
     if args.only == "host_slice":
         hs = bench_host_slice(wrs, W, ctx, reps=100)
         log(f"host_slice only: host slices {hs['host_slice_ms']:.3f} ms/call, "
@@ -1134,6 +1218,8 @@ def main():
     rows = bench_rows(wrs, ctx, args.rows_reps)
     log("host-slice drop-in: whisper-tiny encoder, f32 host slices")
     host_slice = bench_host_slice(wrs, W, ctx)
+    log("reference microbenchmark shapes, f32")
+    ref_shapes = bench_reference_shapes(wrs, ctx)
     copy_gbs = copy_bandwidth()
     read_gbs = read_bandwidth(ctx)
 
@@ -1163,6 +1249,8 @@ def main():
         cpu["linear"] = cpu_baseline_linear(lcfg, n)
         log(f"cpu baseline: oracle f16_linear, one decoder layer's projections, {n} threads")
         cpu["stream"] = cpu_baseline_stream(scfg, n)
+        log(f"cpu baseline: oracle flash_attention_2 at the reference shapes, {n} threads")
+        cpu["reference_shapes"] = cpu_baseline_reference_shapes(info)
 
     L0 = W.SMALL_SELF_DECODE.ctx
     self_floor = sweep.pop("floor", None)
@@ -1249,6 +1337,10 @@ def main():
         },
         "row_kernels": rows,
         "host_slice": host_slice,
+        "reference_shapes": {
+            "workload": "flash_attention_2 at the reference microbenchmark's (t_q, t_kv), "
+                        "6 heads x 64, f32, no mask",
+            "gpu": ref_shapes, "cpu_baseline": cpu.get("reference_shapes")},
         "device": {"name": props.name, "cu": props.multi_processor_count,
                    "copy_GBps": round(copy_gbs, 1), "read_GBps": round(read_gbs, 1)},
         "host": info,

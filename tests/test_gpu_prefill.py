@@ -413,7 +413,7 @@ def test_prefill_rescale_paths(wrs, ctx, profile):
     assert maxerr(got, ref) <= TOL16
 
 
-# ---- the reference benchmark's largest shape ------------------------------------
+# ---- the reference microbenchmark's shapes ------------------------------------
 
 def _bench_inputs(orc, t_q, t_kv, d_model):
     # crates/tensor/tests/bench_flash_attention_tiled.rs:142-146: one xorshift
@@ -422,18 +422,20 @@ def _bench_inputs(orc, t_q, t_kv, d_model):
     return rng.fill(t_q * d_model), rng.fill(t_kv * d_model), rng.fill(t_kv * d_model)
 
 
-def test_host_slice_bench_shape_4096(wrs, orc, ctx):
-    # (4096, 4096), 6 heads of 64 (bench_flash_attention_tiled.rs:19-25) through
-    # the f32 drop-in: the oracle's tiled and materialized results at 1e-5
-    t, H, dm = 4096, 6, 384
-    note("host-slice flash_attention_2 t_q=t_kv=4096, 6 heads, f32")
-    q, k, v = _bench_inputs(orc, t, t, dm)
-    out = np.full(t * dm, np.nan, np.float32)
-    wrs.flash_attention_2(q, k, v, t, t, H, dm, False, out, ctx=ctx)
-    tiled = np.zeros(t * dm, np.float32)
-    orc.flash_attention_2(q, k, v, t, t, H, dm, False, tiled)
-    mat = np.zeros(t * dm, np.float32)
-    orc.materialized_attention(q, k, v, t, t, H, dm, mat)
+@pytest.mark.parametrize("t_q,t_kv", [(1500, 1500), (64, 1500), (4096, 4096)])
+def test_host_slice_bench_shapes(wrs, orc, ctx, t_q, t_kv):
+    # every (t_q, t_kv) of the reference microbenchmark, 6 heads of 64
+    # (bench_flash_attention_tiled.rs:19-25), with its inputs, through the f32
+    # drop-in: the oracle's tiled and materialized results at 1e-5
+    H, dm = 6, 384
+    note(f"host-slice flash_attention_2 t_q={t_q} t_kv={t_kv}, 6 heads, f32")
+    q, k, v = _bench_inputs(orc, t_q, t_kv, dm)
+    out = np.full(t_q * dm, np.nan, np.float32)
+    wrs.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, out, ctx=ctx)
+    tiled = np.zeros(t_q * dm, np.float32)
+    orc.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, tiled)
+    mat = np.zeros(t_q * dm, np.float32)
+    orc.materialized_attention(q, k, v, t_q, t_kv, H, dm, mat)
     e_t, e_m = maxerr(out, tiled), maxerr(out, mat)
     note(f"  max|gpu - tiled| = {e_t:.3e}, max|gpu - materialized| = {e_m:.3e}")
     assert e_t <= TOL32 and e_m <= TOL32
