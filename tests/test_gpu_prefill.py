@@ -28,10 +28,12 @@ def ctx(wrs):
     return c
 
 
-@pytest.fixture(params=[128, 256], ids=["wg128", "wg256"])
+@pytest.fixture(params=[32, 128, 256], ids=["ks32", "wg128", "wg256"])
 def schedule(request, ctx):
-    """Both workgroup sizes of the 16-bit kernel on the same shapes: small grids
-    normally take 128-query workgroups, large ones 256."""
+    """Every schedule of the 16-bit kernel on the same shapes: by default
+    grids of more than one round of 128-query workgroups take 256-query ones,
+    grids that occupy fewer than half the CUs the key split (32 queries, four
+    waves over the keys), the rest 128-query workgroups."""
     ctx.set_schedule(prefill_queries=request.param)
     yield request.param
     ctx.set_schedule()

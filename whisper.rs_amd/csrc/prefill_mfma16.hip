@@ -733,6 +733,355 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   }
 }
 
+// K1s: key split for grids of 128-query workgroups that occupy fewer than
+// half the CUs (one whisper-tiny or -base encoder window: 72 or 96 blocks).
+// There, every wave of the 128-query kernel carries its 32 queries through
+// all keys while most SIMDs idle. A key-split workgroup runs one 32-query block with 4 waves that
+// take its 32-key steps in turn (step j on wave j % 4), each with its own
+// online softmax, so a block's keys run on four SIMDs and the grid has four
+// times the workgroups. The step arithmetic is K1's (S^T = K Q^T on 32x32x16
+// MFMAs, weights exp2(c s - m) packed to f16, row sums on the matrix pipe,
+// the same lazy rescale, O^T += V^T P^T); the operands move differently,
+// since the waves share no keys: each wave loads its K rows straight into
+// registers (a 16-byte load per lane and 16 d is the A-operand layout of the
+// score MFMA) and moves its V rows into its own ring of four 32-key LDS slots
+// with buffer_load ... lds (the transposed reads need them in LDS), three
+// steps ahead of the step it computes. The waves then merge their (max, sum,
+// O) in LDS by the log-sum-exp rule (exp2 domain).
+constexpr int kKsQ = 32;                 // queries per key-split workgroup
+constexpr int kKsRing = 4;               // V slots per wave; steps in flight
+constexpr int kKsStepH = 32 * 64;        // 16-bit elements of one 32-key V step: 4 KiB
+constexpr int kKsPitch = 68;             // merge rows: floats per query row of O
+
+template <typename T>
+__global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64_ks(PrefillArgs a, int n_qblk) {
+  __shared__ __attribute__((aligned(128))) uint16_t Vr[kWaves * kKsRing * kKsStepH];
+  __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
+  static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Vr), "f32 tiles fit in the V rings");
+  static_assert(kKsQ * kKsPitch * 4 + 2 * kKsQ * 4 <= kKsRing * kKsStepH * 2,
+                "a wave's merge rows fit in its ring");
+
+  const int lid = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
+  const int qblk = lid % n_qblk;
+  const int bh = lid / n_qblk;
+  const int h = bh % a.n_heads;
+  const int b = bh / a.n_heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r32 = lane & 31, hl = lane >> 5;
+  if (tid == 0) nonfinite = 0;
+
+  const T* qp = static_cast<const T*>(a.q) + b * a.lq.bs + h * a.lq.hs;
+  const T* kp = static_cast<const T*>(a.k) + b * a.lk.bs + h * a.lk.hs;
+  const T* vp = static_cast<const T*>(a.v) + b * a.lv.bs + h * a.lv.hs;
+
+  // Every global load of this kernel is inline asm and waited for with
+  // explicit vmcnt counts: K lands in registers while V lands in LDS by DMA,
+  // and the compiler, counting only the loads it sees, would wait for later
+  // steps' K too. A loaded register is read only after its wait and an empty
+  // asm that redefines it.
+  // This lane's query: column r32 of the block's S^T (the same in all waves).
+  const int q0 = qblk * kKsQ + r32;
+  u32x4 qf[4] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+  if (q0 < a.t_q) {
+    const T* row = qp + static_cast<int64_t>(q0) * a.lq.rs + hl * 8;
+#pragma unroll
+    for (int dk = 0; dk < 4; ++dk)
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qf[dk]) : "v"(row + dk * 16) : "memory");
+  }
+  int kv_end = a.t_kv;
+  if (a.causal) {
+    const int last = min(qblk * kKsQ + kKsQ, a.t_q) - 1 + a.q_pos_offset;
+    kv_end = min(kv_end, last + 1);
+  }
+  const int nsteps = (kv_end + 31) / 32;
+  // This wave's steps j = wave + 4 i, i < ni.
+  const int ni = nsteps > wave ? (nsteps - wave + 3) / 4 : 0;
+  // First 32-key step that needs a mask.
+  int first_masked = a.t_kv / 32;
+  if (a.causal) first_masked = min(first_masked, (qblk * kKsQ + a.q_pos_offset + 1) / 32);
+
+  // K: lane (r32, hl) loads key 32 j + r32, d 16 dk + 8 hl .. +8, through a
+  // range-checked buffer (keys past t_kv read as zero).
+  const u32x4 krs = buffer_rsrc(kp, static_cast<uint32_t>(((a.t_kv - 1) * a.lk.rs + 64) * 2));
+  const uint32_t kofs = static_cast<uint32_t>((r32 * a.lk.rs + 8 * hl) * 2);
+  const uint32_t kstep = static_cast<uint32_t>(32 * a.lk.rs * 2);
+  // V: 8 rows (1 KiB) per DMA, lane i carrying row i/8, chunk i%8 of them,
+  // stored with K1's chunk swizzle.
+  const u32x4 vrs = buffer_rsrc(vp, static_cast<uint32_t>(((a.t_kv - 1) * a.lv.rs + 64) * 2));
+  uint32_t vofs[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int crow = 8 * r + (lane >> 3);
+    vofs[r] = static_cast<uint32_t>((crow * a.lv.rs + (((lane & 7) ^ swz(crow)) * 8)) * 2);
+  }
+  const uint32_t vstep = static_cast<uint32_t>(32 * a.lv.rs * 2);
+  const uint32_t ring = lds_addr(Vr) + wave * (kKsRing * kKsStepH * 2);
+  u32x4 kr[kKsRing][4];  // K of the steps in flight, by ring slot
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    const int j = wave + 4 * i;
+    const int slot = i % kKsRing;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(ring + slot * (kKsStepH * 2));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dma16(vrs, dst + 1024 * r, vofs[r] + j * vstep);
+    const uint32_t ko = kofs + j * kstep;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(kr[slot][0]) : "v"(ko), "s"(krs)
+                 : "memory");
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:32" : "=v"(kr[slot][1])
+                 : "v"(ko), "s"(krs) : "memory");
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:64" : "=v"(kr[slot][2])
+                 : "v"(ko), "s"(krs) : "memory");
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:96" : "=v"(kr[slot][3])
+                 : "v"(ko), "s"(krs) : "memory");
+  };
+  // After a wait that covers its loads: the registers of a slot hold K.
+  auto landed = [&](int slot) __attribute__((always_inline)) {
+    asm volatile("" : "+v"(kr[slot][0]), "+v"(kr[slot][1]), "+v"(kr[slot][2]), "+v"(kr[slot][3]));
+  };
+  // bf16 V -> f16 in place, once the step's rows have landed.
+  auto convert = [&](int i) __attribute__((always_inline)) {
+    if constexpr (Elem<T>::kConvertV) {
+      uint16_t* base = Vr + (wave * kKsRing + i % kKsRing) * kKsStepH;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        u32x4* p = reinterpret_cast<u32x4*>(base + r * 512 + lane * 8);
+        *p = Elem<T>::to_f16(*p);
+      }
+    }
+  };
+  // V^T operands of step i (K1's transposed reads, on a 32-row slot).
+  const int g4 = lane >> 4, t4 = lane & 15;
+  const int vr0 = 4 * (g4 >> 1) + (t4 >> 2), vc0 = 2 * (g4 & 1) + ((t4 & 3) >> 1);
+  const uint32_t voff0 = static_cast<uint32_t>(vr0 * 128 + ((vc0 ^ swz(vr0)) * 16) + 8 * (t4 & 1));
+  auto vfetch = [&](int i, u32x2 (&va)[8]) __attribute__((always_inline)) {
+    const uint32_t vb = ring + (i % kKsRing) * (kKsStepH * 2) + voff0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const uint32_t x = (vb ^ (64u * cc + 32u * e)) + 1024u * e;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) va[4 * k2 + 2 * cc + e] = read_tr_at(x + 2048u * k2);
+      }
+  };
+
+  const float c = a.scale * kLog2e;
+  f32x16 o[2] = {f32x16{}, f32x16{}};
+  float m = kNoMax, l = 0.f;
+  f32x16 sbuf[2];
+  u32x4 pb[2];
+  u32x2 va[8];
+  f32x4 ls;
+  auto qk = [&](const u32x4 (&ka)[4], f32x16& s) __attribute__((always_inline)) {
+    s = f32x16{};
+#pragma unroll
+    for (int dk = 0; dk < 4; ++dk) s = Elem<T>::mfma(ka[dk], qf[dk], s);
+  };
+  auto mask = [&](int j, f32x16& s) __attribute__((always_inline)) {
+    const int qpos = q0 + a.q_pos_offset;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = 32 * j + 8 * (i >> 2) + 4 * hl + (i & 3);
+      s[i] = ((kk >= a.t_kv) | ((a.causal != 0) & (kk > qpos))) ? -INFINITY : s[i];
+    }
+  };
+  auto weights = [&](const f32x16& s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const f32x2 pp = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * k2 + 2 * w], c, -m)),
+                          __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * k2 + 2 * w + 1], c, -m))};
+        pb[k2][w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pp, f16x2));
+      }
+  };
+  const _Float16 rs_one = ((lane >> 2) & 1) == ((lane >> 4) & 1) ? 1.0f16 : 0.0f16;
+  const f16x8 rs_sel = {rs_one, rs_one, rs_one, rs_one, rs_one, rs_one, rs_one, rs_one};
+  auto row_sums = [&]() __attribute__((always_inline)) {
+    const f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        rs_sel, __builtin_bit_cast(f16x8, pb[0]), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    ls = __builtin_amdgcn_mfma_f32_16x16x32_f16(rs_sel, __builtin_bit_cast(f16x8, pb[1]), acc, 0,
+                                                0, 0);
+  };
+  auto pv = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const u32x4 v0 = {va[4 * k2].x, va[4 * k2].y, va[4 * k2 + 1].x, va[4 * k2 + 1].y};
+      const u32x4 v1 = {va[4 * k2 + 2].x, va[4 * k2 + 2].y, va[4 * k2 + 3].x, va[4 * k2 + 3].y};
+      o[0] = mfma_f16(v0, pb[k2], o[0]);
+      o[1] = mfma_f16(v1, pb[k2], o[1]);
+    }
+  };
+  // K1's lazy rescale on the step's intact scores (see the file header).
+  auto settle = [&](const f32x16& s) __attribute__((always_inline)) {
+    const bool need = __builtin_bit_cast(uint32_t, ls[0]) >
+                      min(__builtin_bit_cast(uint32_t, l) + 0x00800000u,
+                          __builtin_bit_cast(uint32_t, kSumLimit));
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      float mr = fmaxf(s[0], s[1]);
+#pragma unroll
+      for (int i = 2; i < 16; i += 2) mr = fmaxf(fmaxf(mr, s[i]), s[i + 1]);
+      const float mx = pair_max(mr) * c;
+      bool moved = false;
+      if (mx > m) {
+        const float alpha = __builtin_amdgcn_exp2f(m - mx);
+        m = mx;
+        l *= alpha;
+        o[0] *= alpha;
+        o[1] *= alpha;
+        moved = true;
+      }
+      if (__builtin_amdgcn_ballot_w64(moved)) {
+        weights(s);
+        row_sums();
+      }
+    }
+    l += ls[0];
+  };
+  auto wait_loads = [&](int i) __attribute__((always_inline)) {
+    // K of step i+1 (and everything issued before it) has landed: the steps
+    // issued after it, up to i+3, stay in flight.
+    const int after = min(ni - 1, i + 3) - (i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (after >= 2)
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (after == 1)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if (ni > 0) {
+    issue(0);
+    if (ni > 1) issue(1);
+    if (ni > 2) issue(2);
+    // q and step 0 landed (steps 1 and 2 may still fly).
+    wait_loads(-1);
+    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]));
+    landed(0);
+    convert(0);
+    qk(kr[0], sbuf[0]);
+    // Step i: P V of step i-1, step i+3's loads into the slot step i-1 used,
+    // S of step i+1, the weights of step i, its V^T reads, its rescale check.
+    auto step = [&](int i, f32x16& s_in, f32x16& s_out) __attribute__((always_inline)) {
+      const int j = wave + 4 * i;
+      if (i >= 1) pv();
+      // The V^T reads of step i-1 have completed (P V waited for them), so
+      // its slot may be overwritten.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (i + 3 < ni) issue(i + 3);
+      if (i + 1 < ni) {
+        wait_loads(i);
+        landed((i + 1) % kKsRing);
+        convert(i + 1);
+        qk(kr[(i + 1) % kKsRing], s_out);
+      }
+      if (j >= first_masked) mask(j, s_in);
+      if (i == 0) {
+        // The reference max from the first two steps' (masked) scores, so
+        // neither forms its weights twice.
+        float mr = fmaxf(s_in[0], s_in[1]);
+#pragma unroll
+        for (int e = 2; e < 16; e += 2) mr = fmaxf(fmaxf(mr, s_in[e]), s_in[e + 1]);
+        if (ni > 1) {
+          if (j + 4 >= first_masked) mask(j + 4, s_out);
+#pragma unroll
+          for (int e = 0; e < 16; e += 2) mr = fmaxf(fmaxf(mr, s_out[e]), s_out[e + 1]);
+        }
+        const float mx = pair_max(mr) * c;
+        if (mx > m) m = mx;
+      }
+      weights(s_in);
+      row_sums();
+      vfetch(i, va);
+      __builtin_amdgcn_sched_barrier(0);
+      settle(s_in);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // Unrolled by the ring length, so every ring index is a constant.
+    for (int i0 = 0; i0 < ni; i0 += kKsRing) {
+#pragma unroll
+      for (int u = 0; u < kKsRing; ++u)
+        if (i0 + u < ni) step(i0 + u, sbuf[u & 1], sbuf[(u + 1) & 1]);
+    }
+    pv();  // the last step's weights
+  }
+
+  // Merge: each wave leaves its O (query-major rows), max and sum in its own
+  // ring, then thread t combines columns 4 (t % 16) .. +4 of queries t / 16
+  // and t / 16 + 16, storing them as 16-byte pieces of whole output rows.
+  // No load of this wave is in flight (a wave without keys has not waited for
+  // its q loads yet), and every wave is done with its ring.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  float* const mw = reinterpret_cast<float*>(Vr + wave * kKsRing * kKsStepH);
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq)
+      *reinterpret_cast<f32x4*>(mw + r32 * kKsPitch + 32 * hf + 8 * gq + 4 * hl) =
+          f32x4{o[hf][4 * gq], o[hf][4 * gq + 1], o[hf][4 * gq + 2], o[hf][4 * gq + 3]};
+  if (hl == 0) {
+    mw[kKsQ * kKsPitch + r32] = m;
+    mw[kKsQ * kKsPitch + kKsQ + r32] = l;
+  }
+  __syncthreads();
+  float chk = 0.f;
+  {
+    const int c16 = tid & 15;
+    float* const ob = a.o + b * a.lo.bs + h * a.lo.hs + 4 * c16;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int mq = (tid >> 4) + 16 * half;
+      const int oq = qblk * kKsQ + mq;
+      float M = kNoMax;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float* t = reinterpret_cast<const float*>(Vr + w * kKsRing * kKsStepH);
+        M = fmaxf(M, t[kKsQ * kKsPitch + mq]);
+      }
+      float L = 0.f;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float* t = reinterpret_cast<const float*>(Vr + w * kKsRing * kKsStepH);
+        // A wave without keys holds the initial max and zero sums.
+        const float e = __builtin_amdgcn_exp2f(t[kKsQ * kKsPitch + mq] - M);
+        L = __builtin_fmaf(e, t[kKsQ * kKsPitch + kKsQ + mq], L);
+        acc += e * *reinterpret_cast<const f32x4*>(t + mq * kKsPitch + 4 * c16);
+      }
+      const f32x4 v = acc * ((L > 0.f) ? 1.f / L : 0.f);
+      if (oq < a.t_q) {
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(oq) * a.lo.rs));
+        if constexpr (Elem<T>::kConvertV) chk += (v[0] + v[1]) + (v[2] + v[3]);
+      }
+    }
+  }
+  if constexpr (Elem<T>::kConvertV) {
+    // bf16 V of magnitude >= 65536 (inf after the f16 conversion): the
+    // block's 32 queries are computed again with the f32 block routine, as
+    // in K1 (the exponent bits tested as an integer, see K1).
+    uint32_t chk_bits = __builtin_bit_cast(uint32_t, chk);
+    asm volatile("" : "+v"(chk_bits));
+    const bool bad = (chk_bits & 0x7f800000u) == 0x7f800000u;
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) nonfinite = 1;
+    __syncthreads();
+    if (nonfinite) {
+      // The block routine's first 32-query wave takes this block: query rows
+      // start at this block's first row, and at most 32 of them exist.
+      PrefillArgs ab = a;
+      ab.q = static_cast<const T*>(a.q) + static_cast<int64_t>(qblk) * kKsQ * a.lq.rs;
+      ab.o = a.o + static_cast<int64_t>(qblk) * kKsQ * a.lo.rs;
+      ab.t_q = min(kKsQ, a.t_q - qblk * kKsQ);
+      ab.q_pos_offset = a.q_pos_offset + qblk * kKsQ;
+      auto& tl = *reinterpret_cast<f32blk::Tiles<2>*>(Vr);
+      f32blk::fa2_block<__bf16, __bf16, 2>(ab, 0, h, b, tl);
+    }
+  }
+}
+
 // Compute units of the current device, read once.
 int64_t device_cus() {
   static const int64_t cus = [] {
@@ -773,15 +1122,34 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
   const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
   if (bh <= 0 || a.t_q <= 0) return hipSuccess;
-  // 256-query workgroups, unless that grid fills less than one round of the
-  // device's resident slots (two per CU): then 128-query workgroups, so more
-  // CUs run two workgroups (two waves per SIMD overlap the softmax VALU work
-  // with the matrix pipe). a.force_queries (128 or 256) forces one schedule.
-  constexpr int kM2 = queries_per_wg<2>();
-  const int64_t nwg2 = ((a.t_q + kM2 - 1) / kM2) * bh;
-  if (a.force_queries == 256 || (a.force_queries == 0 && nwg2 >= 2 * device_cus()))
+  // 256-query workgroups, unless 128-query workgroups fit in one round of the
+  // device's resident slots (two per CU): then those, so more CUs run two
+  // workgroups (two waves per SIMD overlap the softmax VALU work with the
+  // matrix pipe); and when those occupy fewer than half the CUs, the key
+  // split (32-query workgroups). Past one round, 128-query workgroups lose to
+  // 256-query ones (large-v3 x4 windows, 960 against 480 workgroups: 67.2
+  // against 57.2 us), and within it the two tie (x2: 35.3 against 35.0 us). The key split streams a block's K/V per
+  // 32 queries, 4x the bytes per FLOP of the 128-query kernel, which caps it
+  // near 50 GB/s per CU: measured, it wins only on such grids (one
+  // whisper-base window, 96 blocks: 18.2 against 21.5 us; one small window,
+  // 144 blocks: 25.4 against 21.3 us). a.force_queries (32, 128 or 256)
+  // forces one schedule.
+  constexpr int kM1 = queries_per_wg<1>();
+  const int64_t nwg1 = ((a.t_q + kM1 - 1) / kM1) * bh;
+  if (a.force_queries == 256 || (a.force_queries == 0 && nwg1 > 2 * device_cus()))
     return launch_qb<2>(a, dt, s);
-  return launch_qb<1>(a, dt, s);
+  if (a.force_queries == 128 || (a.force_queries == 0 && 2 * nwg1 >= device_cus()))
+    return launch_qb<1>(a, dt, s);
+  const int n_qblk = (a.t_q + kKsQ - 1) / kKsQ;
+  const int64_t nwg = n_qblk * bh;
+  if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (dt == kF16)
+    hipLaunchKernelGGL((fa2_prefill_d64_ks<_Float16>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(kThreads), 0, s, a, n_qblk);
+  else
+    hipLaunchKernelGGL((fa2_prefill_d64_ks<__bf16>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(kThreads), 0, s, a, n_qblk);
+  return hipGetLastError();
 }
 
 }  // namespace wrs
