@@ -173,6 +173,25 @@ def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True):
     return cfg, ms, tflops, (q, k, v), settled
 
 
+def bench_one_window(wrs, W, ctx, steps, warmup):
+    """The encoder attention of one 30 s window per call (the reference's
+    encoder runs one window at a time): whisper-base (72 workgroups' worth of
+    work at 128 queries, which takes the key split) and large-v3, each also
+    under the 128-query schedule for comparison."""
+    res = {}
+    for cfg in (W.BASE_ENCODER_1, W.LARGE_ENCODER_1):
+        _, ms, tf, _, _ = bench_encoder(wrs, W, ctx, steps, warmup, cfg=cfg, settle=False)
+        ctx.set_schedule(prefill_queries=128)
+        try:
+            _, ms128, tf128, _, _ = bench_encoder(wrs, W, ctx, steps, warmup, cfg=cfg, settle=False)
+        finally:
+            ctx.set_schedule()
+        res[cfg.name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                         "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4),
+                         "wg128_us": round(ms128 * 1e3, 2), "wg128_TFLOPs": round(tf128, 1)}
+    return res
+
+
 def _replay_time_us(g, reps, launches_per_replay):
     import torch
     for _ in range(3):
@@ -1129,7 +1148,7 @@ def main():
     ap.add_argument("--rows-reps", type=int, default=50)
     ap.add_argument("--only", choices=["encoder", "encoder_base", "decode", "decode_self",
                                        "capture", "linear", "stream", "rows", "host_slice",
-                                       "reference_shapes", "traffic"],
+                                       "reference_shapes", "one_window", "traffic"],
                     default=None,
                     help="run one workload only (for profiling); prints no JSON line")
     args = ap.parse_args()
@@ -1149,6 +1168,9 @@ def main():
 
     if args.only == "traffic":
         run_traffic_legs(wrs, W, ctx)
+        return
+    if args.only == "one_window":
+        log(f"one window: {bench_one_window(wrs, W, ctx, args.steps, max(args.warmup, 100))}")
         return
     if args.only in ("encoder", "encoder_base"):
         cfg = W.LARGE_ENCODER if args.only == "encoder" else W.BASE_ENCODER
@@ -1206,6 +1228,7 @@ def main():
     cfg, ms, tflops, qkv, settled = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
     bcfg, bms, btflops, bqkv, bsettled = bench_encoder(wrs, W, ctx, args.steps, args.warmup,
                                                        cfg=W.BASE_ENCODER)
+    one_window = bench_one_window(wrs, W, ctx, args.steps, max(args.warmup, 100))
     dcfg, us, gbs, floor = bench_decode(wrs, W, ctx, args.decode_reps)
     sweep = bench_decode_self(wrs, W, ctx, args.decode_reps)
     ccfg, cus, cgbs = bench_capture(wrs, W, ctx, args.capture_reps)
@@ -1282,6 +1305,7 @@ def main():
                               traffic_bytes("encoder_base")),
             "cpu_baseline": cpu.get("encoder_base"),
         },
+        "encoder_one_window": one_window,
         "decode_cross": {
             "workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s",
             "us_per_launch": round(us, 3), "launches_per_step": dcfg.n_layers,

@@ -199,6 +199,11 @@ LARGE_V3_ALIGNMENT_HEADS = ((7, 0), (10, 17), (12, 18), (13, 12), (16, 1), (17, 
 TINY_ENCODER = Encoder("whisper-tiny encoder self-attention, f32", 1, 6, 1500, "f32",
                        qk_prescale=64.0 ** -0.25)
 BASE_ENCODER = Encoder("whisper-base encoder self-attention x4 windows, f16", 4, 8, 1500, "f16")
+# one 30 s window per call, as the reference's encoder runs it
+BASE_ENCODER_1 = Encoder("whisper-base encoder self-attention, one window, f16", 1, 8, 1500,
+                         "f16")
+LARGE_ENCODER_1 = Encoder("whisper-large-v3 encoder self-attention, one window, bf16 outliers",
+                          1, 20, 1500, "bf16", sigma=0.5, outliers=13)
 SMALL_SELF_DECODE = SelfDecode("whisper-small self-attention decode, beam 5", 5, 12, 224)
 LARGE_CROSS_DECODE = CrossDecode("whisper-large-v3 cross-attention decode, beam 5", 5, 20, 1500,
                                  32)
