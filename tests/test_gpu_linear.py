@@ -103,11 +103,13 @@ def test_decode_weight_stream(wrs, orc, ctx, n_tokens, n_in, n_out, x_dt, out_dt
         assert (np.abs(got - rt) <= tol).all()
 
 
-def test_linear_f32_row_scaling(wrs, orc, ctx):
+@pytest.mark.parametrize("n_in", [256, 3200])
+def test_linear_f32_row_scaling(wrs, orc, ctx, n_in):
     """Rows of very different magnitude (1e-30 .. 1e30, a zero row) stay exact:
-    each row is scaled by a power of two before the f16 split."""
-    note("linear f32 row scaling")
-    n_in, n_out = 256, 64
+    each row is scaled by a power of two before the f16 split (rows held in
+    registers, and longer rows staged by the whole workgroup)."""
+    note(f"linear f32 row scaling, {n_in} columns")
+    n_out = 64
     rng = np.random.default_rng(11)
     x = rng.standard_normal((6, n_in)).astype(np.float32)
     x *= np.array([[1e-30], [1e-6], [1.0], [7e4], [1e30], [0.0]], np.float32)

@@ -893,9 +893,10 @@ hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStre
       (x_dt == kF32 || x_dt == kF16)) {
     // Tiles of T features, T chosen so that the tiles of all groups just
     // cover one workgroup per CU (a d x d matrix measured fastest that way:
-    // two smaller tiles per CU stage x twice); up to as many workgroups as fit
-    // at once (LDS and registers decide) share larger matrices, looping over
-    // tiles.
+    // two smaller tiles per CU stage x twice), or exactly k per CU when one
+    // per CU would need more than 16 features: a 5120-row matrix in 16-feature
+    // tiles gave 64 CUs two tiles and the rest one. Up to as many workgroups
+    // as fit at once (LDS and registers decide) share the tiles, looping.
     const dim3 gblock(64 * kGmWaves);
 #define WRS_GM_L(XT, OT, LN)                                                                  \
   {                                                                                           \
@@ -913,7 +914,9 @@ hipError_t launch_gemv_f16w(const GemvArgs& a, DType x_dt, DType out_dt, hipStre
         per_cu < 1)                                                                           \
       per_cu = 1;                                                                             \
     const int64_t rows = static_cast<int64_t>(a.n_out) * a.n_groups;                         \
-    const int T = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(16, (rows + n_cu - 1) / n_cu))); \
+    const int64_t per_cu_tiles = (rows + 16 * n_cu - 1) / (16 * n_cu);                      \
+    const int T = static_cast<int>(std::max<int64_t>(                                        \
+        1, std::min<int64_t>(16, (rows + per_cu_tiles * n_cu - 1) / (per_cu_tiles * n_cu)))); \
     const int n_tiles = (a.n_out + T - 1) / T;                                                \
     const dim3 ggrid(std::min(n_tiles, n_cu * std::min(per_cu, 2)), a.n_groups);              \
     hipLaunchKernelGGL((gemv_f16w_mfma<XT, OT, LN>), ggrid, gblock, gm_lds, s, a, T);         \
