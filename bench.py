@@ -133,10 +133,13 @@ def time_best(a, reps: int = REPS) -> float:
     return best
 
 
-def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True):
+def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True, graph=0):
     """One prefill launch over all windows per step, inputs resident in HBM:
     a time-bounded clock-settle phase, `warmup` untimed steps, then `steps`
-    timed steps between two events on the launch stream."""
+    timed steps between two events on the launch stream. With `graph` > 0
+    the steps are replays of a HIP graph of that many launches (checked
+    against the eager result first), for launches shorter than the host's
+    own call path."""
     import torch
     cfg = cfg or W.LARGE_ENCODER
     log(f"encoder: generating {cfg.name}")
@@ -147,9 +150,28 @@ def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True):
     out = torch.empty((B, T, dm), dtype=torch.float32, device="cuda")
     lay = wrs.token_major(T, dm, 64)
 
-    def step():
+    def launch():
         wrs.prefill(qd, kd, vd, out, batch=B, n_heads=cfg.n_heads, t_q=T, t_kv=T, d_head=64,
                     q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+
+    step, per_step = launch, 1
+    if graph > 0:
+        launch()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ctx.use_torch_stream()
+            for _ in range(graph):
+                launch()
+        ctx.use_torch_stream()
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(out, eager):
+            raise RuntimeError("graph replay of the encoder launches differs from eager")
+        step, per_step = g.replay, graph
+        steps, warmup = max(1, -(-steps // graph)), -(-warmup // graph)
 
     settled = 0
     if settle:
@@ -160,13 +182,14 @@ def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True):
         step()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    log(f"encoder: timing {steps} steps")
+    log(f"encoder: timing {steps * per_step} steps")
     start.record()
     for _ in range(steps):
         step()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms = start.elapsed_time(end) / (steps * per_step)
+    settled *= per_step
     tflops = cfg.flops() / (ms * 1e-3) / 1e12
     log(f"encoder: {cfg.name}: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s "
         f"({tflops / PEAK_BF16_TFLOPS:.3f} of peak; settle {settled} launches)")
@@ -175,15 +198,21 @@ def bench_encoder(wrs, W, ctx, steps, warmup, cfg=None, settle=True):
 
 def bench_one_window(wrs, W, ctx, steps, warmup):
     """The encoder attention of one 30 s window per call (the reference's
-    encoder runs one window at a time): whisper-base (72 workgroups' worth of
-    work at 128 queries, which takes the key split) and large-v3, each also
-    under the 128-query schedule for comparison."""
+    encoder runs one window at a time): whisper-base (96 blocks of 128
+    queries, fewer than half the CUs, which takes the key split) and large-v3
+    (240 blocks, which takes key halves), each also under the 128-query
+    schedule for comparison. The first leg settles the clocks; the launches
+    are replayed from HIP graphs of 25, since one window's launch is shorter
+    than the host's call path."""
     res = {}
-    for cfg in (W.BASE_ENCODER_1, W.LARGE_ENCODER_1):
-        _, ms, tf, _, _ = bench_encoder(wrs, W, ctx, steps, warmup, cfg=cfg, settle=False)
+    steps = max(steps, 100)
+    for i, cfg in enumerate((W.BASE_ENCODER_1, W.LARGE_ENCODER_1)):
+        _, ms, tf, _, _ = bench_encoder(wrs, W, ctx, steps, warmup, cfg=cfg, settle=i == 0,
+                                        graph=25)
         ctx.set_schedule(prefill_queries=128)
         try:
-            _, ms128, tf128, _, _ = bench_encoder(wrs, W, ctx, steps, warmup, cfg=cfg, settle=False)
+            _, ms128, tf128, _, _ = bench_encoder(wrs, W, ctx, steps, warmup, cfg=cfg,
+                                                  settle=False, graph=25)
         finally:
             ctx.set_schedule()
         res[cfg.name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),

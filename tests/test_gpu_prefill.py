@@ -28,12 +28,14 @@ def ctx(wrs):
     return c
 
 
-@pytest.fixture(params=[32, 128, 256], ids=["ks32", "wg128", "wg256"])
+@pytest.fixture(params=[32, 64, 128, 256], ids=["ks32", "kh64", "wg128", "wg256"])
 def schedule(request, ctx):
     """Every schedule of the 16-bit kernel on the same shapes: by default
-    grids of more than one round of 128-query workgroups take 256-query ones,
-    grids that occupy fewer than half the CUs the key split (32 queries, four
-    waves over the keys), the rest 128-query workgroups."""
+    grids of more than two 128-query blocks per CU take 256-query
+    workgroups, more than one 128-query workgroups, at least half the CUs
+    key halves (eight waves on 128 queries, the halves taking alternate
+    64-key tiles), fewer the key split (32 queries, four waves over the
+    keys)."""
     ctx.set_schedule(prefill_queries=request.param)
     yield request.param
     ctx.set_schedule()

@@ -10,6 +10,9 @@
 //
 // Work decomposition: one workgroup = 4 waves = 256 queries of one
 // (window, head), two workgroups per CU; each wave owns two 32-query blocks.
+// Smaller grids take 128-query workgroups (one block per wave), 8-wave ones
+// whose halves split the keys, or the key split (K1s, below);
+// launch_prefill_mfma16 picks by grid size.
 // Computing S^T = K Q^T (keys on the MFMA M axis) puts one query per lane, and
 // the S^T accumulator registers are, after exp2 and packing, exactly the B
 // operand of O^T += V^T P^T. Every K and V^T operand read from LDS feeds the
@@ -234,14 +237,22 @@ constexpr bool pipe_order_ok() {
 }
 static_assert(pipe_order_ok<1>() && pipe_order_ok<2>(), "pipelined step order");
 
-template <typename T, int QB>
-__global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, int n_qblk) {
+// KH = 2 (one query block per wave only): the workgroup is two halves of four
+// waves that share its 128 queries and split its keys, half hf taking the
+// 64-key tiles hf, hf + 2, ... through its own LDS ring; the halves then
+// merge their (max, sum, O) lane by lane (their registers hold the same
+// queries in the same layout). For grids of at most one such workgroup per
+// CU, it puts two waves on every SIMD of the CUs in use instead of one.
+template <typename T, int QB, int KH>
+__global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(PrefillArgs a,
+                                                                        int n_qblk) {
+  static_assert(KH == 1 || (KH == 2 && QB == 1), "key halves with one query block per wave");
   constexpr int kQB = QB;
   constexpr int kM = queries_per_wg<QB>();
   typedef f32x16 SBlk[kQB];
   typedef u32x4 PBlk[kQB][2];
-  __shared__ __attribute__((aligned(128))) uint16_t Ks[kNB * kTileH];
-  __shared__ __attribute__((aligned(128))) uint16_t Vs[kNB * kTileH];
+  __shared__ __attribute__((aligned(128))) uint16_t Ks[KH * kNB * kTileH];
+  __shared__ __attribute__((aligned(128))) uint16_t Vs[KH * kNB * kTileH];
   __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
   static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Ks), "f32 tiles fit in the K buffers");
   static_assert(kThreads == f32blk::kThreads && kM % f32blk::kM == 0, "whole f32 blocks");
@@ -256,6 +267,12 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hl = lane >> 5;
+  // Key half of this wave, its place among the half's four waves, and the
+  // half's tile ring.
+  const int half = KH == 2 ? (wave >> 2) : 0;
+  const int w4 = wave & 3;
+  uint16_t* const Kh = Ks + half * (kNB * kTileH);
+  uint16_t* const Vh = Vs + half * (kNB * kTileH);
   // Cleared before the first tile barrier; set only after the last one.
   if (tid == 0) nonfinite = 0;
 
@@ -264,7 +281,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const T* vp = static_cast<const T*>(a.v) + b * a.lv.bs + h * a.lv.hs;
 
   // This lane's queries: column r32 of each of the wave's S^T blocks.
-  const int q0 = qblk * kM + wave * (32 * kQB) + r32;
+  const int q0 = qblk * kM + w4 * (32 * kQB) + r32;
   u32x4 qf[kQB][4];
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
@@ -284,8 +301,14 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     const int last = min(qblk * kM + kM, a.t_q) - 1 + a.q_pos_offset;
     kv_end = min(kv_end, last + 1);
   }
-  const int n_tiles = (kv_end + kN - 1) / kN;
-  const int nh = 2 * n_tiles;  // 32-key steps
+  const int n_tiles_all = (kv_end + kN - 1) / kN;
+  // This half's tiles (local tile t is tile KH t + half of the block's keys)
+  // and the most that any half has.
+  const int n_tiles = (n_tiles_all - half + KH - 1) / KH;
+  const int t_most = (n_tiles_all + KH - 1) / KH;
+  const int nh = 2 * n_tiles;  // this half's 32-key steps
+  // The block's 32-key step of this half's step j.
+  auto gstep = [&](int j) { return 2 * (KH * (j >> 1) + half) + (j & 1); };
   // First step that needs a mask: keys past t_kv, or (causal) past the first
   // query of the workgroup.
   int first_masked = a.t_kv / 32;
@@ -296,7 +319,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   uint32_t kofs[kRowGroups], vofs[kRowGroups];
 #pragma unroll
   for (int r = 0; r < kRowGroups; ++r) {
-    const int crow = kRowsPerWave * wave + 8 * r + (lane >> 3);
+    const int crow = kRowsPerWave * w4 + 8 * r + (lane >> 3);
     const int cch = (lane & 7) ^ swz(crow);
     kofs[r] = static_cast<uint32_t>((crow * a.lk.rs + cch * 8) * 2);
     vofs[r] = static_cast<uint32_t>((crow * a.lv.rs + cch * 8) * 2);
@@ -305,21 +328,23 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const uint32_t vstep = static_cast<uint32_t>(kN * a.lv.rs * 2);
   const u32x4 krs = buffer_rsrc(kp, static_cast<uint32_t>(((a.t_kv - 1) * a.lk.rs + 64) * 2));
   const u32x4 vrs = buffer_rsrc(vp, static_cast<uint32_t>(((a.t_kv - 1) * a.lv.rs + 64) * 2));
-  const uint32_t ks_lds = lds_addr(Ks) + wave * kRowsPerWave * 128;
-  const uint32_t vs_lds = lds_addr(Vs) + wave * kRowsPerWave * 128;
+  const uint32_t ks_lds = lds_addr(Kh) + w4 * kRowsPerWave * 128;
+  const uint32_t vs_lds = lds_addr(Vh) + w4 * kRowsPerWave * 128;
   auto issue_tile = [&](int t) {
     const uint32_t buf = __builtin_amdgcn_readfirstlane((t % kNB) * (kTileH * 2));
 #pragma unroll
-    for (int r = 0; r < kRowGroups; ++r) dma16(krs, ks_lds + buf + 1024 * r, kofs[r] + t * kstep);
+    for (int r = 0; r < kRowGroups; ++r)
+      dma16(krs, ks_lds + buf + 1024 * r, kofs[r] + (KH * t + half) * kstep);
 #pragma unroll
-    for (int r = 0; r < kRowGroups; ++r) dma16(vrs, vs_lds + buf + 1024 * r, vofs[r] + t * vstep);
+    for (int r = 0; r < kRowGroups; ++r)
+      dma16(vrs, vs_lds + buf + 1024 * r, vofs[r] + (KH * t + half) * vstep);
   };
   // bf16 V -> f16 in place: this wave's own rows, whose loads have landed.
   auto convert_tile = [&](int t) {
     if constexpr (Elem<T>::kConvertV) {
 #pragma unroll
       for (int r = 0; r < kRowGroups; ++r) {
-        u32x4* p = reinterpret_cast<u32x4*>(Vs + (t % kNB) * kTileH + wave * kRowsPerWave * 64 +
+        u32x4* p = reinterpret_cast<u32x4*>(Vh + (t % kNB) * kTileH + w4 * kRowsPerWave * 64 +
                                             r * 512 + lane * 8);
         *p = Elem<T>::to_f16(*p);
       }
@@ -340,7 +365,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   const int vr0 = 4 * (g >> 1) + (t4 >> 2), vc0 = 2 * (g & 1) + ((t4 & 3) >> 1);
   const uint32_t voff0 = static_cast<uint32_t>(vr0 * 128 + ((vc0 ^ swz(vr0)) * 16) + 8 * (t4 & 1));
   auto k_base = [&](int step) {
-    return lds_addr(Ks) + ((step >> 1) % kNB) * (kTileH * 2) + (step & 1) * 32 * 128 + koff0;
+    return lds_addr(Kh) + ((step >> 1) % kNB) * (kTileH * 2) + (step & 1) * 32 * 128 + koff0;
   };
   auto kfetch = [&](int step, u32x4 (&ka)[4]) {
     const uint32_t kb = k_base(step);
@@ -349,7 +374,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   };
   auto vfetch = [&](int step, u32x2 (&va)[8]) {
     const uint32_t vb =
-        lds_addr(Vs) + ((step >> 1) % kNB) * (kTileH * 2) + (step & 1) * 32 * 128 + voff0;
+        lds_addr(Vh) + ((step >> 1) % kNB) * (kTileH * 2) + (step & 1) * 32 * 128 + voff0;
 #pragma unroll
     for (int e = 0; e < 2; ++e)
 #pragma unroll
@@ -516,13 +541,13 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
       // P V of step j-1 first: its weights' registers are then free for step j's.
       if (j >= 1) pv(va, pb);
       if (j + 1 < nh) qk(ka, s_out);
-      if (j >= first_masked) mask_step(j, s_in);
+      if (gstep(j) >= first_masked) mask_step(gstep(j), s_in);
       if (j == 0) {
         // First step: take the reference max from the (masked) scores of the
         // first two steps now (those of step 1 were just issued above), so the
         // weights of both are formed against their exact max and once.
         const bool two = nh > 1;
-        if (two && 1 >= first_masked) mask_step(1, s_out);
+        if (two && gstep(1) >= first_masked) mask_step(gstep(1), s_out);
 #pragma unroll
         for (int jb = 0; jb < kQB; ++jb) {
           float mr = fmaxf(s_in[jb][0], s_in[jb][1]);
@@ -648,12 +673,47 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     };
     // Tile 0 (no PV yet), full tiles (both steps complete and unmasked), then
     // the tail.
-    const int t_full_end = min(n_tiles - 1, first_masked / 2);
+    const int t_full_end = min(n_tiles - 1, (first_masked / 2 - half + KH - 1) / KH);
     tile(Part{}, 0);
     int t = 1;
     for (; t < t_full_end; ++t) tile(Full{}, t);
     for (; t < n_tiles; ++t) tile(Part{}, t);
     pv(va, pb);  // the last step's weights
+  }
+  if constexpr (KH == 2) {
+    // The halves meet at equally many barriers: the one with fewer tiles
+    // waits out the other's (the prologue's barrier, then one per tile).
+    const int mine = n_tiles > 0 ? 1 + n_tiles : 0;
+    const int most = t_most > 0 ? 1 + t_most : 0;
+    for (int i = mine; i < most; ++i) tile_barrier();
+    // No wave reads a tile any more and every tile load has landed: half 1
+    // leaves its O, max and sum in its own ring (O in the K tiles as
+    // [wave][register][lane], max and sum in the V tiles), and half 0 folds
+    // them into its own by the log-sum-exp rule (exp2 domain). A half
+    // without keys holds the initial max and zero sums.
+    float* const xo = reinterpret_cast<float*>(Ks + kNB * kTileH);
+    float* const xm = reinterpret_cast<float*>(Vs + kNB * kTileH);
+    if (half == 1) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xo[(w4 * 32 + 16 * hf + i) * 64 + lane] = o[0][hf][i];
+      xm[(2 * w4) * 64 + lane] = m[0];
+      xm[(2 * w4 + 1) * 64 + lane] = l[0];
+    }
+    __syncthreads();
+    if (half == 0) {
+      const float m1 = xm[(2 * w4) * 64 + lane], l1 = xm[(2 * w4 + 1) * 64 + lane];
+      const float mm = fmaxf(m[0], m1);
+      const float e0 = __builtin_amdgcn_exp2f(m[0] - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
+      l[0] = l[0] * e0 + l1 * e1;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          o[0][hf][i] = o[0][hf][i] * e0 + xo[(w4 * 32 + 16 * hf + i) * 64 + lane] * e1;
+      m[0] = mm;
+    }
   }
 
   // The outputs leave as whole 256-byte query rows. Each wave stages its
@@ -663,11 +723,13 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   // instruction would write 32 bytes to each of 32 rows.
   constexpr int kStageBytes = 32 * kQB * 256;
   static_assert(kWaves * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
-  char* const stage = wave * kStageBytes < static_cast<int>(sizeof(Ks))
-                          ? reinterpret_cast<char*>(Ks) + wave * kStageBytes
-                          : reinterpret_cast<char*>(Vs) + (wave * kStageBytes - sizeof(Ks));
+  // (With key halves, half 0's waves store: their rows fit in its K tiles.)
+  char* const stage = w4 * kStageBytes < static_cast<int>(sizeof(Ks))
+                          ? reinterpret_cast<char*>(Ks) + w4 * kStageBytes
+                          : reinterpret_cast<char*>(Vs) + (w4 * kStageBytes - sizeof(Ks));
   // Sum of this lane's outputs: inf/NaN when any of them is.
   float chk = 0.f;
+  if (half == 0) {
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
     // l is the whole row sum in both lanes of the query (the row sums are).
@@ -697,7 +759,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   {
     const int c16 = lane & 15;
-    const int qw = qblk * kM + wave * (32 * kQB);  // the wave's first query
+    const int qw = qblk * kM + w4 * (32 * kQB);  // the wave's first query
     float* const ob = a.o + b * a.lo.bs + h * a.lo.hs + 4 * c16;
 #pragma unroll
     for (int k = 0; k < 8 * kQB; ++k) {
@@ -710,6 +772,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
         __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(qw + rr) * a.lo.rs));
     }
   }
+  }  // half 0
   if constexpr (Elem<T>::kConvertV) {
     // A bf16 V value of magnitude >= 65536 is inf after the f16 conversion and
     // turns the rows that meet it into inf/NaN (a finite sum that overflows
@@ -727,8 +790,13 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_prefill_d64(PrefillArgs a, in
     if (nonfinite) {
       auto& tl = *reinterpret_cast<f32blk::Tiles<2>*>(Ks);
       constexpr int kBlocks = kM / f32blk::kM;
-      f32blk::fa2_block<__bf16, __bf16, 2>(a, kBlocks * qblk, h, b, tl);
-      if constexpr (kBlocks == 2) f32blk::fa2_block<__bf16, __bf16, 2>(a, 2 * qblk + 1, h, b, tl);
+      // With key halves the routine runs on 512 threads: the second half's
+      // waves take query rows past the block, which t_q clipped to the block
+      // makes empty (they only share its tile loads and barriers).
+      PrefillArgs ab = a;
+      if constexpr (KH == 2) ab.t_q = min(a.t_q, (qblk + 1) * kM);
+      f32blk::fa2_block<__bf16, __bf16, 2>(ab, kBlocks * qblk, h, b, tl);
+      if constexpr (kBlocks == 2) f32blk::fa2_block<__bf16, __bf16, 2>(ab, 2 * qblk + 1, h, b, tl);
     }
   }
 }
@@ -1093,17 +1161,17 @@ int64_t device_cus() {
   return cus;
 }
 
-template <int QB>
+template <int QB, int KH>
 hipError_t launch_qb(const PrefillArgs& a, DType dt, hipStream_t s) {
   constexpr int kM = queries_per_wg<QB>();
   const int n_qblk = (a.t_q + kM - 1) / kM;
   const int64_t nwg = n_qblk * static_cast<int64_t>(a.n_heads) * a.batch;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads * KH);
   if (dt == kF16)
-    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB>), grid, block, 0, s, a, n_qblk);
+    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB, KH>), grid, block, 0, s, a, n_qblk);
   else
-    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB>), grid, block, 0, s, a, n_qblk);
+    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB, KH>), grid, block, 0, s, a, n_qblk);
   return hipGetLastError();
 }
 
@@ -1122,24 +1190,32 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
   const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
   if (bh <= 0 || a.t_q <= 0) return hipSuccess;
-  // 256-query workgroups, unless 128-query workgroups fit in one round of the
-  // device's resident slots (two per CU): then those, so more CUs run two
-  // workgroups (two waves per SIMD overlap the softmax VALU work with the
-  // matrix pipe); and when those occupy fewer than half the CUs, the key
-  // split (32-query workgroups). Past one round, 128-query workgroups lose to
-  // 256-query ones (large-v3 x4 windows, 960 against 480 workgroups: 67.2
-  // against 57.2 us), and within it the two tie (x2: 35.3 against 35.0 us). The key split streams a block's K/V per
-  // 32 queries, 4x the bytes per FLOP of the 128-query kernel, which caps it
-  // near 50 GB/s per CU: measured, it wins only on such grids (one
-  // whisper-base window, 96 blocks: 18.2 against 21.5 us; one small window,
-  // 144 blocks: 25.4 against 21.3 us). a.force_queries (32, 128 or 256)
-  // forces one schedule.
+  // By the number of 128-query blocks (measured on encoder windows, 1500
+  // frames, one box):
+  // - more than two per CU: 256-query workgroups (large-v3 x4 windows, 480
+  //   against 960 workgroups: 57.2 against 67.2 us);
+  // - more than one per CU: 128-query workgroups, two per CU, so two waves
+  //   share each SIMD and overlap the softmax VALU work with the matrix pipe
+  //   (large-v3 x2: 35.5 us, a tie with 256-query ones);
+  // - at least half the CUs: 128-query workgroups of eight waves whose halves
+  //   split the keys, one per CU, which keeps two waves per SIMD on a grid
+  //   that gives each CU at most one block (one large-v3 window, 240 blocks:
+  //   21.4 against 25.1 us; one small window, 144 blocks: 18.3 against 21.7);
+  // - fewer: the key split (32-query workgroups), which spreads a block over
+  //   four CUs (one whisper-base window, 96 blocks: 18.0 against 18.4 us with
+  //   key halves). It streams a block's K/V per 32 queries, 4x the bytes per
+  //   FLOP of the 128-query kernel, which caps it near 50 GB/s per CU.
+  // a.force_queries forces one schedule by its queries per four waves: 256,
+  // 128, 64 (key halves) or 32 (key split).
   constexpr int kM1 = queries_per_wg<1>();
   const int64_t nwg1 = ((a.t_q + kM1 - 1) / kM1) * bh;
-  if (a.force_queries == 256 || (a.force_queries == 0 && nwg1 > 2 * device_cus()))
-    return launch_qb<2>(a, dt, s);
-  if (a.force_queries == 128 || (a.force_queries == 0 && 2 * nwg1 >= device_cus()))
-    return launch_qb<1>(a, dt, s);
+  const int cus = device_cus();
+  if (a.force_queries == 256 || (a.force_queries == 0 && nwg1 > 2 * cus))
+    return launch_qb<2, 1>(a, dt, s);
+  if (a.force_queries == 128 || (a.force_queries == 0 && nwg1 > cus))
+    return launch_qb<1, 1>(a, dt, s);
+  if (a.force_queries == 64 || (a.force_queries == 0 && 2 * nwg1 >= cus))
+    return launch_qb<1, 2>(a, dt, s);
   const int n_qblk = (a.t_q + kKsQ - 1) / kKsQ;
   const int64_t nwg = n_qblk * bh;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
