@@ -1203,7 +1203,8 @@ def main():
         return
     if args.only in ("encoder", "encoder_base"):
         cfg = W.LARGE_ENCODER if args.only == "encoder" else W.BASE_ENCODER
-        _, ms, tflops, _, n = bench_encoder(wrs, W, ctx, args.steps, args.warmup, cfg=cfg)
+        _, ms, tflops, _, n = bench_encoder(wrs, W, ctx, args.steps, args.warmup, cfg=cfg,
+                                            graph=0 if args.only == "encoder" else 25)
         calibration_copy()
         log(f"{args.only} only: {ms:.4f} ms/step, {tflops:.1f} TFLOP/s (settle {n} launches)")
         return
@@ -1255,8 +1256,10 @@ def main():
         return
 
     cfg, ms, tflops, qkv, settled = bench_encoder(wrs, W, ctx, args.steps, args.warmup)
+    # whisper-base x4 (~30 us a launch) from graph replays, like one window:
+    # its launch is about as long as the host's call path.
     bcfg, bms, btflops, bqkv, bsettled = bench_encoder(wrs, W, ctx, args.steps, args.warmup,
-                                                       cfg=W.BASE_ENCODER)
+                                                       cfg=W.BASE_ENCODER, graph=25)
     one_window = bench_one_window(wrs, W, ctx, args.steps, max(args.warmup, 100))
     dcfg, us, gbs, floor = bench_decode(wrs, W, ctx, args.decode_reps)
     sweep = bench_decode_self(wrs, W, ctx, args.decode_reps)

@@ -28,14 +28,13 @@ def ctx(wrs):
     return c
 
 
-@pytest.fixture(params=[32, 64, 128, 256], ids=["ks32", "kh64", "wg128", "wg256"])
+@pytest.fixture(params=[32, -128, -256, 128, 256], ids=["ks32", "kh128", "kh256", "wg128", "wg256"])
 def schedule(request, ctx):
-    """Every schedule of the 16-bit kernel on the same shapes: by default
-    grids of more than two 128-query blocks per CU take 256-query
-    workgroups, more than one 128-query workgroups, at least half the CUs
-    key halves (eight waves on 128 queries, the halves taking alternate
-    64-key tiles), fewer the key split (32 queries, four waves over the
-    keys)."""
+    """Every schedule of the 16-bit kernel on the same shapes: 4-wave
+    workgroups of 256 or 128 queries, the same blocks on 8-wave workgroups
+    whose halves take alternate 64-key tiles (key halves, -256 / -128), and
+    the key split (32 queries, four waves over the keys). By default the
+    grid size picks one."""
     ctx.set_schedule(prefill_queries=request.param)
     yield request.param
     ctx.set_schedule()

@@ -246,7 +246,7 @@ static_assert(pipe_order_ok<1>() && pipe_order_ok<2>(), "pipelined step order");
 template <typename T, int QB, int KH>
 __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(PrefillArgs a,
                                                                         int n_qblk) {
-  static_assert(KH == 1 || (KH == 2 && QB == 1), "key halves with one query block per wave");
+  static_assert(KH == 1 || KH == 2, "one or two key halves");
   constexpr int kQB = QB;
   constexpr int kM = queries_per_wg<QB>();
   typedef f32x16 SBlk[kQB];
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   // Key half of this wave, its place among the half's four waves, and the
   // half's tile ring.
   const int half = KH == 2 ? (wave >> 2) : 0;
-  const int w4 = wave & 3;
+  const int w4 = KH == 2 ? (wave & 3) : wave;
   uint16_t* const Kh = Ks + half * (kNB * kTileH);
   uint16_t* const Vh = Vs + half * (kNB * kTileH);
   // Cleared before the first tile barrier; set only after the last one.
@@ -687,33 +687,46 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
     const int most = t_most > 0 ? 1 + t_most : 0;
     for (int i = mine; i < most; ++i) tile_barrier();
     // No wave reads a tile any more and every tile load has landed: half 1
-    // leaves its O, max and sum in its own ring (O in the K tiles as
-    // [wave][register][lane], max and sum in the V tiles), and half 0 folds
-    // them into its own by the log-sum-exp rule (exp2 domain). A half
-    // without keys holds the initial max and zero sums.
-    float* const xo = reinterpret_cast<float*>(Ks + kNB * kTileH);
-    float* const xm = reinterpret_cast<float*>(Vs + kNB * kTileH);
+    // leaves its O (in the V rings, as [wave][block][register][lane]) and its
+    // max and sum (in its K ring), and half 0 folds them into its own by the
+    // log-sum-exp rule (exp2 domain). A half without keys holds the initial
+    // max and zero sums.
+    float* const xo = reinterpret_cast<float*>(Vs);
+    float* const xm = reinterpret_cast<float*>(Ks + kNB * kTileH);
+    static_assert(kWaves * kQB * 32 * 64 * 4 <= static_cast<int>(sizeof(Vs)), "O fits");
+    static_assert(kWaves * kQB * 2 * 64 * 4 <= kNB * kTileH * 2, "max and sum fit");
     if (half == 1) {
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+      for (int j = 0; j < kQB; ++j) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xo[(w4 * 32 + 16 * hf + i) * 64 + lane] = o[0][hf][i];
-      xm[(2 * w4) * 64 + lane] = m[0];
-      xm[(2 * w4 + 1) * 64 + lane] = l[0];
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            xo[((w4 * kQB + j) * 32 + 16 * hf + i) * 64 + lane] = o[j][hf][i];
+        xm[((w4 * kQB + j) * 2) * 64 + lane] = m[j];
+        xm[((w4 * kQB + j) * 2 + 1) * 64 + lane] = l[j];
+      }
     }
     __syncthreads();
     if (half == 0) {
-      const float m1 = xm[(2 * w4) * 64 + lane], l1 = xm[(2 * w4 + 1) * 64 + lane];
-      const float mm = fmaxf(m[0], m1);
-      const float e0 = __builtin_amdgcn_exp2f(m[0] - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
-      l[0] = l[0] * e0 + l1 * e1;
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+      for (int j = 0; j < kQB; ++j) {
+        const float m1 = xm[((w4 * kQB + j) * 2) * 64 + lane];
+        const float l1 = xm[((w4 * kQB + j) * 2 + 1) * 64 + lane];
+        const float mm = fmaxf(m[j], m1);
+        const float e0 = __builtin_amdgcn_exp2f(m[j] - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
+        l[j] = l[j] * e0 + l1 * e1;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          o[0][hf][i] = o[0][hf][i] * e0 + xo[(w4 * 32 + 16 * hf + i) * 64 + lane] * e1;
-      m[0] = mm;
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            o[j][hf][i] = o[j][hf][i] * e0 + xo[((w4 * kQB + j) * 32 + 16 * hf + i) * 64 + lane] * e1;
+        m[j] = mm;
+      }
     }
+    // The output staging below overwrites the K rings, where the max and sum
+    // were.
+    if constexpr (kQB == 2) __syncthreads();
   }
 
   // The outputs leave as whole 256-byte query rows. Each wave stages its
@@ -723,7 +736,7 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   // instruction would write 32 bytes to each of 32 rows.
   constexpr int kStageBytes = 32 * kQB * 256;
   static_assert(kWaves * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
-  // (With key halves, half 0's waves store: their rows fit in its K tiles.)
+  // (With key halves, half 0's waves store: their rows fit in the K rings.)
   char* const stage = w4 * kStageBytes < static_cast<int>(sizeof(Ks))
                           ? reinterpret_cast<char*>(Ks) + w4 * kStageBytes
                           : reinterpret_cast<char*>(Vs) + (w4 * kStageBytes - sizeof(Ks));
@@ -791,12 +804,15 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
       auto& tl = *reinterpret_cast<f32blk::Tiles<2>*>(Ks);
       constexpr int kBlocks = kM / f32blk::kM;
       // With key halves the routine runs on 512 threads: the second half's
-      // waves take query rows past the block, which t_q clipped to the block
-      // makes empty (they only share its tile loads and barriers).
+      // waves take query rows past the 128-query block, which t_q clipped to
+      // the block makes empty (they only share its tile loads and barriers).
       PrefillArgs ab = a;
-      if constexpr (KH == 2) ab.t_q = min(a.t_q, (qblk + 1) * kM);
+      if constexpr (KH == 2) ab.t_q = min(a.t_q, (kBlocks * qblk + 1) * f32blk::kM);
       f32blk::fa2_block<__bf16, __bf16, 2>(ab, kBlocks * qblk, h, b, tl);
-      if constexpr (kBlocks == 2) f32blk::fa2_block<__bf16, __bf16, 2>(ab, 2 * qblk + 1, h, b, tl);
+      if constexpr (kBlocks == 2) {
+        if constexpr (KH == 2) ab.t_q = min(a.t_q, (2 * qblk + 2) * f32blk::kM);
+        f32blk::fa2_block<__bf16, __bf16, 2>(ab, 2 * qblk + 1, h, b, tl);
+      }
     }
   }
 }
@@ -1190,32 +1206,38 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
   const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
   if (bh <= 0 || a.t_q <= 0) return hipSuccess;
-  // By the number of 128-query blocks (measured on encoder windows, 1500
+  // By the number n of 128-query blocks (measured on encoder windows, 1500
   // frames, one box):
-  // - more than two per CU: 256-query workgroups (large-v3 x4 windows, 480
-  //   against 960 workgroups: 57.2 against 67.2 us);
-  // - more than one per CU: 128-query workgroups, two per CU, so two waves
-  //   share each SIMD and overlap the softmax VALU work with the matrix pipe
-  //   (large-v3 x2: 35.5 us, a tie with 256-query ones);
-  // - at least half the CUs: 128-query workgroups of eight waves whose halves
-  //   split the keys, one per CU, which keeps two waves per SIMD on a grid
-  //   that gives each CU at most one block (one large-v3 window, 240 blocks:
-  //   21.4 against 25.1 us; one small window, 144 blocks: 18.3 against 21.7);
+  // - n > 2 per CU: 256-query workgroups, two per CU (large-v3 x4 windows,
+  //   480 against 960 workgroups: 58.1 against 66.6 us);
+  // - 1.25 per CU <= n <= 2 per CU: 256-query blocks on 8-wave workgroups
+  //   whose halves split the keys, one per CU (whisper-base x4: 29.3 against
+  //   30.4 us with 128-query workgroups; large-v3 x2: 32.8 against 34.8). Two
+  //   waves then share every SIMD, where 4-wave workgroups would leave CUs
+  //   holding one of them alone;
+  // - 1 per CU < n < 1.25 per CU: 128-query workgroups, two per CU (whisper-
+  //   small x2, 288 blocks: 28.6 against 29.3 us);
+  // - half the CUs <= n <= 1 per CU: 128-query blocks on 8-wave workgroups
+  //   with key halves (one large-v3 window, 240 blocks: 20.9 against 25.7 us;
+  //   one whisper-small window, 144 blocks: 18.7 against 21.3);
   // - fewer: the key split (32-query workgroups), which spreads a block over
-  //   four CUs (one whisper-base window, 96 blocks: 18.0 against 18.4 us with
+  //   four CUs (one whisper-tiny window, 72 blocks: 18.2 against 18.7 us with
   //   key halves). It streams a block's K/V per 32 queries, 4x the bytes per
   //   FLOP of the 128-query kernel, which caps it near 50 GB/s per CU.
-  // a.force_queries forces one schedule by its queries per four waves: 256,
-  // 128, 64 (key halves) or 32 (key split).
+  // Below two blocks per CU a launch is one round of workgroups (~20-30 us),
+  // in which each workgroup's fixed costs (q and the first tiles, the output
+  // rows) are not hidden. a.force_queries forces one schedule: 256 or 128 queries per 4-wave
+  // workgroup, -256 or -128 the same queries on 8 waves with key halves, 32
+  // the key split.
   constexpr int kM1 = queries_per_wg<1>();
   const int64_t nwg1 = ((a.t_q + kM1 - 1) / kM1) * bh;
-  const int cus = device_cus();
-  if (a.force_queries == 256 || (a.force_queries == 0 && nwg1 > 2 * cus))
-    return launch_qb<2, 1>(a, dt, s);
-  if (a.force_queries == 128 || (a.force_queries == 0 && nwg1 > cus))
-    return launch_qb<1, 1>(a, dt, s);
-  if (a.force_queries == 64 || (a.force_queries == 0 && 2 * nwg1 >= cus))
-    return launch_qb<1, 2>(a, dt, s);
+  const int64_t cus = device_cus();
+  const bool by_grid = a.force_queries == 0;
+  if (a.force_queries == 256 || (by_grid && nwg1 > 2 * cus)) return launch_qb<2, 1>(a, dt, s);
+  if (a.force_queries == -256 || (by_grid && 4 * nwg1 >= 5 * cus))
+    return launch_qb<2, 2>(a, dt, s);
+  if (a.force_queries == 128 || (by_grid && nwg1 > cus)) return launch_qb<1, 1>(a, dt, s);
+  if (a.force_queries == -128 || (by_grid && 2 * nwg1 >= cus)) return launch_qb<1, 2>(a, dt, s);
   const int n_qblk = (a.t_q + kKsQ - 1) / kKsQ;
   const int64_t nwg = n_qblk * bh;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
