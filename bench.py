@@ -837,7 +837,7 @@ def bench_reference_shapes(wrs, ctx, reps=20):
             "host_slice_GFLOPs": round(gflop / host_ms * 1e3, 1),
             "device_resident_ms": round(dev_ms, 4),
             "device_resident_GFLOPs": round(gflop / dev_ms * 1e3, 1),
-            "pcie_bytes_per_call": 4 * (q.nbytes + k.nbytes + v.nbytes + out.nbytes)}
+            "pcie_bytes_per_call": q.nbytes + k.nbytes + v.nbytes + out.nbytes}
         log(f"reference shape ({t_q}, {t_kv}) x {H} heads: host slices {host_ms:.3f} ms, "
             f"device-resident {dev_ms * 1e3:.1f} us ({gflop / dev_ms:.1f} TFLOP/s)")
         del qd, kd, vd, od
