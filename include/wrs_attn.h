@@ -72,10 +72,10 @@ int wrs_attn_synchronize(wrs_attn_ctx *ctx);
  * on it beyond floating-point summation order. No reference counterpart: the
  * reference's tiling is fixed (Q_TILE = KV_TILE = 128, attention.rs:13,26).
  * prefill_queries: queries per workgroup of the f16/bf16 kernel: 256 or 128
- * (four waves), -256 or -128 for that many queries on eight waves whose
- * halves take alternate 64-key tiles (key halves), 32 for the key split
- * (four waves share a 32-query block's keys), or 0 to choose by grid size
- * (the default). f32_split: -1 chooses by
+ * (four waves), -256, -192 or -128 for that many queries on eight, twelve or
+ * eight waves whose halves take alternate 64-key tiles (key halves), 32 for
+ * the key split (four waves share a 32-query block's keys), or 0 to choose
+ * by grid size (the default). f32_split: -1 chooses by
  * grid size (the default), 0 runs 128-query blocks, 1 the four-wave key
  * split, 2..4 the key split over that many waves. Other values: WRS_EINVAL. */
 int wrs_attn_set_schedule(wrs_attn_ctx *ctx, int prefill_queries, int f32_split);

@@ -85,8 +85,8 @@ class Context:
     def set_schedule(self, prefill_queries: int = 0, f32_split: int = -1) -> None:
         """Work decomposition of this context's prefill calls
         (``wrs_attn_set_schedule``): queries per workgroup of the f16/bf16
-        kernel (256 or 128; -256 or -128 for key halves on eight waves; 32 for
-        the key split; 0 = by grid size) and the
+        kernel (256 or 128; -256, -192 or -128 for key halves on 8 or 12
+        waves; 32 for the key split; 0 = by grid size) and the
         f32 kernel's key split
         (-1 = by grid size, 0 = 128-query blocks, 1..4 = key split)."""
         self.check(self._lib.wrs_attn_set_schedule(self.handle, int(prefill_queries),

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, in
   __shared__ Tiles<DB> tl;
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = lid / n_qblk;
-  fa2_block<QT, KT, DB>(a, lid % n_qblk, bh % a.n_heads, bh / a.n_heads, tl);
+  fa2_block<QT, KT, DB>(a, (lid % n_qblk) * f32blk::kM, bh % a.n_heads, bh / a.n_heads, tl);
 }
 
 // Small grids of 128-query blocks (whisper-tiny's encoder: 12 blocks x 6

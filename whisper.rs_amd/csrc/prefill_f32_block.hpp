@@ -38,10 +38,12 @@ struct Tiles {
   float v[kN * P];
 };
 
-// One 128-query block: query rows [qblk*128, qblk*128+128) of head h of
-// batch entry b. DB: number of 32-wide blocks covering d_head (<= 32*DB).
-template <typename QT, typename KT, int DB>
-__device__ inline void fa2_block(const PrefillArgs& a, int qblk, int h, int b, Tiles<DB>& tl) {
+// One block of query rows: [q_begin, q_begin + 32*NW) of head h of batch
+// entry b, run by NW waves (4 in the f32 kernel: a 128-query block), rows at
+// or past a.t_q left alone. DB: number of 32-wide blocks covering d_head
+// (<= 32*DB).
+template <typename QT, typename KT, int DB, int NW = 4>
+__device__ inline void fa2_block(const PrefillArgs& a, int q_begin, int h, int b, Tiles<DB>& tl) {
   constexpr int D = 32 * DB;
   constexpr int P = Tiles<DB>::P;
   float* Ks = tl.k;
@@ -56,7 +58,7 @@ __device__ inline void fa2_block(const PrefillArgs& a, int qblk, int h, int b, T
   const KT* kp = static_cast<const KT*>(a.k) + b * a.lk.bs + h * a.lk.hs;
   const KT* vp = static_cast<const KT*>(a.v) + b * a.lv.bs + h * a.lv.hs;
 
-  const int qi = qblk * kM + wave * 32 + r32;
+  const int qi = q_begin + wave * 32 + r32;
   const int qpos = qi + a.q_pos_offset;
   // B operand of step kk: Q[qi][2*kk + hl].
   float qf[D / 2];
@@ -68,7 +70,7 @@ __device__ inline void fa2_block(const PrefillArgs& a, int qblk, int h, int b, T
 
   int kv_end = a.t_kv;
   if (a.causal) {
-    const int last = min(qblk * kM + kM, a.t_q) - 1 + a.q_pos_offset;
+    const int last = min(q_begin + 32 * NW, a.t_q) - 1 + a.q_pos_offset;
     kv_end = min(kv_end, last + 1);
   }
 
@@ -79,7 +81,7 @@ __device__ inline void fa2_block(const PrefillArgs& a, int qblk, int h, int b, T
 
   for (int j0 = 0; j0 < kv_end; j0 += kN) {
     __syncthreads();
-    for (int e = tid; e < kN * D; e += kThreads) {
+    for (int e = tid; e < kN * D; e += 64 * NW) {
       const int key = e / D, d = e % D;
       float kv = 0.f, vv = 0.f;
       if (j0 + key < a.t_kv && d < dh) {

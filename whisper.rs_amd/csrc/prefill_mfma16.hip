@@ -197,10 +197,11 @@ __device__ inline void wait_tiles() {
 }
 
 // QB: 32-query blocks per wave (2, or 1 for grids below one round of
-// workgroups); a workgroup holds 32 * QB * kWaves queries.
-template <int QB>
+// workgroups); QW: waves that share a workgroup's queries (4, or 6); a
+// workgroup holds 32 * QB * QW queries.
+template <int QB, int QW = kWaves>
 constexpr int queries_per_wg() {
-  return 32 * QB * kWaves;
+  return 32 * QB * QW;
 }
 
 // Software pipeline of a full 32-key step (see full_step in the kernel): one
@@ -237,25 +238,28 @@ constexpr bool pipe_order_ok() {
 }
 static_assert(pipe_order_ok<1>() && pipe_order_ok<2>(), "pipelined step order");
 
-// KH = 2 (one query block per wave only): the workgroup is two halves of four
-// waves that share its 128 queries and split its keys, half hf taking the
-// 64-key tiles hf, hf + 2, ... through its own LDS ring; the halves then
-// merge their (max, sum, O) lane by lane (their registers hold the same
-// queries in the same layout). For grids of at most one such workgroup per
-// CU, it puts two waves on every SIMD of the CUs in use instead of one.
-template <typename T, int QB, int KH>
-__global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(PrefillArgs a,
-                                                                        int n_qblk) {
+// KH = 2 (key halves): the workgroup is two halves of QW waves that share its
+// 32 * QB * QW queries and split its keys, half hf taking the 64-key tiles
+// hf, hf + 2, ... through its own LDS ring; the halves then merge their
+// (max, sum, O) lane by lane (their registers hold the same queries in the
+// same layout). For grids of at most one such workgroup per CU, it puts two
+// waves (three with QW = 6) on every SIMD of the CUs in use instead of one.
+// With QW = 6 the first four waves of a half move its tiles and the other
+// two only compute.
+template <typename T, int QB, int KH, int QW = kWaves>
+__global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
+    PrefillArgs a, int n_qblk) {
   static_assert(KH == 1 || KH == 2, "one or two key halves");
+  static_assert(QW == kWaves || (QW == 6 && QB == 1 && KH == 2),
+                "six query waves: one block each, key halves");
   constexpr int kQB = QB;
-  constexpr int kM = queries_per_wg<QB>();
+  constexpr int kM = queries_per_wg<QB, QW>();
   typedef f32x16 SBlk[kQB];
   typedef u32x4 PBlk[kQB][2];
   __shared__ __attribute__((aligned(128))) uint16_t Ks[KH * kNB * kTileH];
   __shared__ __attribute__((aligned(128))) uint16_t Vs[KH * kNB * kTileH];
   __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
   static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Ks), "f32 tiles fit in the K buffers");
-  static_assert(kThreads == f32blk::kThreads && kM % f32blk::kM == 0, "whole f32 blocks");
 
   const int lid = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
   const int qblk = lid % n_qblk;
@@ -269,8 +273,10 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   const int r32 = lane & 31, hl = lane >> 5;
   // Key half of this wave, its place among the half's four waves, and the
   // half's tile ring.
-  const int half = KH == 2 ? (wave >> 2) : 0;
-  const int w4 = KH == 2 ? (wave & 3) : wave;
+  const int half = KH == 1 ? 0 : QW == kWaves ? (wave >> 2) : wave / QW;
+  const int wq = KH == 1 ? wave : QW == kWaves ? (wave & 3) : wave - QW * half;
+  // The first four waves of a half move its tiles (16 rows of each apiece).
+  const bool mover = QW == kWaves || wq < kWaves;
   uint16_t* const Kh = Ks + half * (kNB * kTileH);
   uint16_t* const Vh = Vs + half * (kNB * kTileH);
   // Cleared before the first tile barrier; set only after the last one.
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   const T* vp = static_cast<const T*>(a.v) + b * a.lv.bs + h * a.lv.hs;
 
   // This lane's queries: column r32 of each of the wave's S^T blocks.
-  const int q0 = qblk * kM + w4 * (32 * kQB) + r32;
+  const int q0 = qblk * kM + wq * (32 * kQB) + r32;
   u32x4 qf[kQB][4];
 #pragma unroll
   for (int j = 0; j < kQB; ++j) {
@@ -319,7 +325,7 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   uint32_t kofs[kRowGroups], vofs[kRowGroups];
 #pragma unroll
   for (int r = 0; r < kRowGroups; ++r) {
-    const int crow = kRowsPerWave * w4 + 8 * r + (lane >> 3);
+    const int crow = kRowsPerWave * wq + 8 * r + (lane >> 3);
     const int cch = (lane & 7) ^ swz(crow);
     kofs[r] = static_cast<uint32_t>((crow * a.lk.rs + cch * 8) * 2);
     vofs[r] = static_cast<uint32_t>((crow * a.lv.rs + cch * 8) * 2);
@@ -328,9 +334,10 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   const uint32_t vstep = static_cast<uint32_t>(kN * a.lv.rs * 2);
   const u32x4 krs = buffer_rsrc(kp, static_cast<uint32_t>(((a.t_kv - 1) * a.lk.rs + 64) * 2));
   const u32x4 vrs = buffer_rsrc(vp, static_cast<uint32_t>(((a.t_kv - 1) * a.lv.rs + 64) * 2));
-  const uint32_t ks_lds = lds_addr(Kh) + w4 * kRowsPerWave * 128;
-  const uint32_t vs_lds = lds_addr(Vh) + w4 * kRowsPerWave * 128;
+  const uint32_t ks_lds = lds_addr(Kh) + wq * kRowsPerWave * 128;
+  const uint32_t vs_lds = lds_addr(Vh) + wq * kRowsPerWave * 128;
   auto issue_tile = [&](int t) {
+    if (!mover) return;
     const uint32_t buf = __builtin_amdgcn_readfirstlane((t % kNB) * (kTileH * 2));
 #pragma unroll
     for (int r = 0; r < kRowGroups; ++r)
@@ -342,9 +349,10 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   // bf16 V -> f16 in place: this wave's own rows, whose loads have landed.
   auto convert_tile = [&](int t) {
     if constexpr (Elem<T>::kConvertV) {
+      if (!mover) return;
 #pragma unroll
       for (int r = 0; r < kRowGroups; ++r) {
-        u32x4* p = reinterpret_cast<u32x4*>(Vh + (t % kNB) * kTileH + w4 * kRowsPerWave * 64 +
+        u32x4* p = reinterpret_cast<u32x4*>(Vh + (t % kNB) * kTileH + wq * kRowsPerWave * 64 +
                                             r * 512 + lane * 8);
         *p = Elem<T>::to_f16(*p);
       }
@@ -693,8 +701,8 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
     // max and zero sums.
     float* const xo = reinterpret_cast<float*>(Vs);
     float* const xm = reinterpret_cast<float*>(Ks + kNB * kTileH);
-    static_assert(kWaves * kQB * 32 * 64 * 4 <= static_cast<int>(sizeof(Vs)), "O fits");
-    static_assert(kWaves * kQB * 2 * 64 * 4 <= kNB * kTileH * 2, "max and sum fit");
+    static_assert(QW * kQB * 32 * 64 * 4 <= static_cast<int>(sizeof(Vs)), "O fits");
+    static_assert(QW * kQB * 2 * 64 * 4 <= kNB * kTileH * 2, "max and sum fit");
     if (half == 1) {
 #pragma unroll
       for (int j = 0; j < kQB; ++j) {
@@ -702,17 +710,17 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
-            xo[((w4 * kQB + j) * 32 + 16 * hf + i) * 64 + lane] = o[j][hf][i];
-        xm[((w4 * kQB + j) * 2) * 64 + lane] = m[j];
-        xm[((w4 * kQB + j) * 2 + 1) * 64 + lane] = l[j];
+            xo[((wq * kQB + j) * 32 + 16 * hf + i) * 64 + lane] = o[j][hf][i];
+        xm[((wq * kQB + j) * 2) * 64 + lane] = m[j];
+        xm[((wq * kQB + j) * 2 + 1) * 64 + lane] = l[j];
       }
     }
     __syncthreads();
     if (half == 0) {
 #pragma unroll
       for (int j = 0; j < kQB; ++j) {
-        const float m1 = xm[((w4 * kQB + j) * 2) * 64 + lane];
-        const float l1 = xm[((w4 * kQB + j) * 2 + 1) * 64 + lane];
+        const float m1 = xm[((wq * kQB + j) * 2) * 64 + lane];
+        const float l1 = xm[((wq * kQB + j) * 2 + 1) * 64 + lane];
         const float mm = fmaxf(m[j], m1);
         const float e0 = __builtin_amdgcn_exp2f(m[j] - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
         l[j] = l[j] * e0 + l1 * e1;
@@ -720,13 +728,13 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
-            o[j][hf][i] = o[j][hf][i] * e0 + xo[((w4 * kQB + j) * 32 + 16 * hf + i) * 64 + lane] * e1;
+            o[j][hf][i] = o[j][hf][i] * e0 + xo[((wq * kQB + j) * 32 + 16 * hf + i) * 64 + lane] * e1;
         m[j] = mm;
       }
     }
-    // The output staging below overwrites the K rings, where the max and sum
-    // were.
-    if constexpr (kQB == 2) __syncthreads();
+    // The output staging below reaches into half 1's K ring, where the max and
+    // sum were, when it needs more than half 0's.
+    if constexpr (QW * 32 * kQB * 256 > kNB * kTileH * 2) __syncthreads();
   }
 
   // The outputs leave as whole 256-byte query rows. Each wave stages its
@@ -735,11 +743,11 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   // then 16 lanes store one row: stored straight from the MFMA layout, one
   // instruction would write 32 bytes to each of 32 rows.
   constexpr int kStageBytes = 32 * kQB * 256;
-  static_assert(kWaves * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
+  static_assert(QW * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
   // (With key halves, half 0's waves store: their rows fit in the K rings.)
-  char* const stage = w4 * kStageBytes < static_cast<int>(sizeof(Ks))
-                          ? reinterpret_cast<char*>(Ks) + w4 * kStageBytes
-                          : reinterpret_cast<char*>(Vs) + (w4 * kStageBytes - sizeof(Ks));
+  char* const stage = wq * kStageBytes < static_cast<int>(sizeof(Ks))
+                          ? reinterpret_cast<char*>(Ks) + wq * kStageBytes
+                          : reinterpret_cast<char*>(Vs) + (wq * kStageBytes - sizeof(Ks));
   // Sum of this lane's outputs: inf/NaN when any of them is.
   float chk = 0.f;
   if (half == 0) {
@@ -772,7 +780,7 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   {
     const int c16 = lane & 15;
-    const int qw = qblk * kM + w4 * (32 * kQB);  // the wave's first query
+    const int qw = qblk * kM + wq * (32 * kQB);  // the wave's first query
     float* const ob = a.o + b * a.lo.bs + h * a.lo.hs + 4 * c16;
 #pragma unroll
     for (int k = 0; k < 8 * kQB; ++k) {
@@ -802,17 +810,17 @@ __global__ __launch_bounds__(kThreads * KH, 2 / KH) void fa2_prefill_d64(Prefill
     __syncthreads();
     if (nonfinite) {
       auto& tl = *reinterpret_cast<f32blk::Tiles<2>*>(Ks);
-      constexpr int kBlocks = kM / f32blk::kM;
-      // With key halves the routine runs on 512 threads: the second half's
-      // waves take query rows past the 128-query block, which t_q clipped to
-      // the block makes empty (they only share its tile loads and barriers).
+      // Every wave runs the routine, 32 query rows each; where that covers
+      // more rows than the workgroup holds (key halves), t_q clipped to the
+      // workgroup's block leaves the extra waves empty (they only share the
+      // routine's tile loads and barriers).
+      constexpr int kNW = QW * KH;
+      constexpr int kRows = 32 * kNW;
       PrefillArgs ab = a;
-      if constexpr (KH == 2) ab.t_q = min(a.t_q, (kBlocks * qblk + 1) * f32blk::kM);
-      f32blk::fa2_block<__bf16, __bf16, 2>(ab, kBlocks * qblk, h, b, tl);
-      if constexpr (kBlocks == 2) {
-        if constexpr (KH == 2) ab.t_q = min(a.t_q, (2 * qblk + 2) * f32blk::kM);
-        f32blk::fa2_block<__bf16, __bf16, 2>(ab, 2 * qblk + 1, h, b, tl);
-      }
+      if constexpr (kRows > kM) ab.t_q = min(a.t_q, qblk * kM + kM);
+#pragma unroll
+      for (int r0 = 0; r0 < kM; r0 += kRows)
+        f32blk::fa2_block<__bf16, __bf16, 2, kNW>(ab, qblk * kM + r0, h, b, tl);
     }
   }
 }
@@ -1177,17 +1185,17 @@ int64_t device_cus() {
   return cus;
 }
 
-template <int QB, int KH>
+template <int QB, int KH, int QW = kWaves>
 hipError_t launch_qb(const PrefillArgs& a, DType dt, hipStream_t s) {
-  constexpr int kM = queries_per_wg<QB>();
+  constexpr int kM = queries_per_wg<QB, QW>();
   const int n_qblk = (a.t_q + kM - 1) / kM;
   const int64_t nwg = n_qblk * static_cast<int64_t>(a.n_heads) * a.batch;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<unsigned>(nwg)), block(kThreads * KH);
+  const dim3 grid(static_cast<unsigned>(nwg)), block(64 * QW * KH);
   if (dt == kF16)
-    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB, KH>), grid, block, 0, s, a, n_qblk);
+    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB, KH, QW>), grid, block, 0, s, a, n_qblk);
   else
-    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB, KH>), grid, block, 0, s, a, n_qblk);
+    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB, KH, QW>), grid, block, 0, s, a, n_qblk);
   return hipGetLastError();
 }
 
@@ -1206,34 +1214,39 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
   const int64_t bh = static_cast<int64_t>(a.n_heads) * a.batch;
   if (bh <= 0 || a.t_q <= 0) return hipSuccess;
-  // By the number n of 128-query blocks (measured on encoder windows, 1500
-  // frames, one box):
+  // By the numbers n and n' of 128- and 192-query blocks (measured on encoder
+  // windows, 1500 frames, one box):
   // - n > 2 per CU: 256-query workgroups, two per CU (large-v3 x4 windows,
-  //   480 against 960 workgroups: 58.1 against 66.6 us);
-  // - 1.25 per CU <= n <= 2 per CU: 256-query blocks on 8-wave workgroups
-  //   whose halves split the keys, one per CU (whisper-base x4: 29.3 against
-  //   30.4 us with 128-query workgroups; large-v3 x2: 32.8 against 34.8). Two
-  //   waves then share every SIMD, where 4-wave workgroups would leave CUs
-  //   holding one of them alone;
-  // - 1 per CU < n < 1.25 per CU: 128-query workgroups, two per CU (whisper-
-  //   small x2, 288 blocks: 28.6 against 29.3 us);
+  //   480 against 960 workgroups: 62.1 against 70.2 us);
+  // - n > 1 per CU >= n': 192-query blocks on 12-wave workgroups whose halves
+  //   split the keys, one per CU (whisper-base x4, 256 blocks: 27.7 against
+  //   31.5 us with 128-query workgroups; whisper-small x2: 23.8 against 29.1).
+  //   Three waves then share every SIMD, where 4-wave workgroups would leave
+  //   CUs holding one of them alone;
+  // - 1.25 per CU <= n <= 2 per CU otherwise: 256-query blocks on 8-wave
+  //   key-halves workgroups (large-v3 x2: 35.1 against 36.4 us);
+  // - 1 per CU < n < 1.25 per CU otherwise: 128-query workgroups, two per CU;
   // - half the CUs <= n <= 1 per CU: 128-query blocks on 8-wave workgroups
-  //   with key halves (one large-v3 window, 240 blocks: 20.9 against 25.7 us;
-  //   one whisper-small window, 144 blocks: 18.7 against 21.3);
+  //   with key halves (one large-v3 window, 240 blocks: 21.5 against 25.7 us;
+  //   one whisper-small window, 144 blocks: 18.6 against 21.4);
   // - fewer: the key split (32-query workgroups), which spreads a block over
-  //   four CUs (one whisper-tiny window, 72 blocks: 18.2 against 18.7 us with
+  //   four CUs (one whisper-tiny window, 72 blocks: 18.3 against 18.4 us with
   //   key halves). It streams a block's K/V per 32 queries, 4x the bytes per
   //   FLOP of the 128-query kernel, which caps it near 50 GB/s per CU.
   // Below two blocks per CU a launch is one round of workgroups (~20-30 us),
   // in which each workgroup's fixed costs (q and the first tiles, the output
-  // rows) are not hidden. a.force_queries forces one schedule: 256 or 128 queries per 4-wave
-  // workgroup, -256 or -128 the same queries on 8 waves with key halves, 32
-  // the key split.
+  // rows) are not hidden. a.force_queries forces one schedule: 256 or 128
+  // queries per 4-wave workgroup, -256, -192 or -128 that many on 8 or 12
+  // waves with key halves, 32 the key split.
   constexpr int kM1 = queries_per_wg<1>();
+  constexpr int kM6 = queries_per_wg<1, 6>();
   const int64_t nwg1 = ((a.t_q + kM1 - 1) / kM1) * bh;
+  const int64_t nwg6 = ((a.t_q + kM6 - 1) / kM6) * bh;
   const int64_t cus = device_cus();
   const bool by_grid = a.force_queries == 0;
   if (a.force_queries == 256 || (by_grid && nwg1 > 2 * cus)) return launch_qb<2, 1>(a, dt, s);
+  if (a.force_queries == -192 || (by_grid && nwg1 > cus && nwg6 <= cus))
+    return launch_qb<1, 2, 6>(a, dt, s);
   if (a.force_queries == -256 || (by_grid && 4 * nwg1 >= 5 * cus))
     return launch_qb<2, 2>(a, dt, s);
   if (a.force_queries == 128 || (by_grid && nwg1 > cus)) return launch_qb<1, 1>(a, dt, s);
