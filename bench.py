@@ -745,6 +745,18 @@ def bench_rows(wrs, ctx, reps):
     return res
 
 
+def host_call_ms(fn, reps: int) -> dict:
+    """Per-call wall times of a synchronous host-slice call, in ms: the
+    median (the figure reported; single calls through pageable host memory
+    now and then stall for tens of milliseconds), the mean and the best."""
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return {"median": float(np.median(ts)), "mean": float(np.mean(ts)), "best": min(ts)}
+
+
 def bench_host_slice(wrs, W, ctx, reps=20):
     """The host-slice drop-in (flash_attention_2 on f32 host slices, PCIe both
     ways) against the same call on device-resident f32 tensors, whisper-tiny
@@ -756,10 +768,9 @@ def bench_host_slice(wrs, W, ctx, reps=20):
     T, H, dm = cfg.t, cfg.n_heads, cfg.d_model
     for _ in range(3):
         wrs.flash_attention_2(q, k, v, T, T, H, dm, False, out, ctx=ctx)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        wrs.flash_attention_2(q, k, v, T, T, H, dm, False, out, ctx=ctx)
-    host_ms = (time.perf_counter() - t0) * 1e3 / reps
+    host = host_call_ms(lambda: wrs.flash_attention_2(q, k, v, T, T, H, dm, False, out, ctx=ctx),
+                        reps)
+    host_ms = host["median"]
     qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
     od = torch.empty_like(qd)
     lay = wrs.token_major(T, dm, 64)
@@ -778,6 +789,8 @@ def bench_host_slice(wrs, W, ctx, reps=20):
     gflop = cfg.flops() / 1e9
     return {"workload": cfg.name, "unit": "GFLOP/s",
             "host_slice_ms": round(host_ms, 3), "host_slice_value": round(gflop / host_ms * 1e3, 1),
+            "host_slice_mean_ms": round(host["mean"], 3),
+            "host_slice_best_ms": round(host["best"], 3),
             "device_resident_ms": round(dev_ms, 4),
             "device_resident_value": round(gflop / dev_ms * 1e3, 1),
             "pcie_bytes_per_call": 4 * q.nbytes}
@@ -801,8 +814,9 @@ def _reference_shape_inputs(t_q, t_kv, n_heads=6):
 
 def bench_reference_shapes(wrs, ctx, reps=20):
     """flash_attention_2 at the reference microbenchmark's shapes, f32, no mask:
-    the host-slice drop-in (PCIe both ways, synchronous) and the same call on
-    device-resident tensors (the f32 prefill kernel), per shape."""
+    the host-slice drop-in (PCIe both ways, synchronous; median per call of
+    `reps`) and the same call on device-resident tensors (the f32 prefill
+    kernel), per shape."""
     import torch
     res = {}
     H = 6
@@ -812,10 +826,9 @@ def bench_reference_shapes(wrs, ctx, reps=20):
         out = np.empty_like(q)
         for _ in range(3):
             wrs.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, out, ctx=ctx)
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            wrs.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, out, ctx=ctx)
-        host_ms = (time.perf_counter() - t0) * 1e3 / reps
+        host = host_call_ms(
+            lambda: wrs.flash_attention_2(q, k, v, t_q, t_kv, H, dm, False, out, ctx=ctx), reps)
+        host_ms = host["median"]
         qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
         od = torch.empty_like(qd)
         lq, lkv = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
@@ -835,6 +848,8 @@ def bench_reference_shapes(wrs, ctx, reps=20):
         res[f"{t_q}x{t_kv}"] = {
             "host_slice_ms": round(host_ms, 4),
             "host_slice_GFLOPs": round(gflop / host_ms * 1e3, 1),
+            "host_slice_mean_ms": round(host["mean"], 4),
+            "host_slice_best_ms": round(host["best"], 4),
             "device_resident_ms": round(dev_ms, 4),
             "device_resident_GFLOPs": round(gflop / dev_ms * 1e3, 1),
             "pcie_bytes_per_call": q.nbytes + k.nbytes + v.nbytes + out.nbytes}
@@ -920,8 +935,9 @@ def calibration_copy():
 
 # kernel-name patterns of each leg in the counter passes (demangled names)
 TRAFFIC_LEGS = {
-    # demangled (fa2_prefill_d64<__bf16>) or mangled (fa2_prefill_d64IDF16b...)
-    "encoder": (r"fa2_prefill_d64(?:<\s*|I)(?:__bf16|bf16|DF16b)", None),
+    # demangled (fa2_prefill_d64<__bf16, ...>) or mangled (fa2_prefill_d64IDF16b...);
+    # rocprofv3's demangler can also print the __bf16 argument as "bool _Accum"
+    "encoder": (r"fa2_prefill_d64(?:<\s*|I)(?:__bf16|bf16|DF16b|bool _Accum)", None),
     "encoder_base": (r"fa2_prefill_d64(?:<\s*|I)(?:_Float16|half|DF16_)", None),
     "decode": (r"decode_f16<\s*5\s*,", None),
     "decode_self": (r"decode_f16<\s*1\s*,", None),
