@@ -73,9 +73,11 @@ int wrs_attn_synchronize(wrs_attn_ctx *ctx);
  * reference's tiling is fixed (Q_TILE = KV_TILE = 128, attention.rs:13,26).
  * prefill_queries: queries per workgroup of the f16/bf16 kernel: 256 or 128
  * (four waves), -256, -192 or -128 for that many queries on eight, twelve or
- * eight waves whose halves take alternate 64-key tiles (key halves), 32 for
- * the key split (four waves share a 32-query block's keys), or 0 to choose
- * by grid size (the default). f32_split: -1 chooses by
+ * eight waves whose halves take alternate 64-key tiles (key halves), -64 for
+ * 128-query blocks on two such workgroups each (merged through context
+ * scratch, allocated at the first such call), 32 for the key split (four
+ * waves share a 32-query block's keys), or 0 to choose by grid size (the
+ * default). f32_split: -1 chooses by
  * grid size (the default), 0 runs 128-query blocks, 1 the four-wave key
  * split, 2..4 the key split over that many waves. Other values: WRS_EINVAL. */
 int wrs_attn_set_schedule(wrs_attn_ctx *ctx, int prefill_queries, int f32_split);
@@ -89,9 +91,14 @@ const char *wrs_attn_status_string(int status);
  * reference allocates per call on the host). Device-resident entry points
  * never allocate once their sizes are reserved; a call that would grow
  * scratch while the context's stream records a graph fails with
- * WRS_ECAPTURE instead. Switching streams (wrs_attn_set_stream) drains the
- * old stream unless either stream is recording a graph. Zero fields are
- * ignored; reserving never shrinks. Synchronous. */
+ * WRS_ECAPTURE instead. One exception needs no reservation:
+ * 16-bit prefill grids of fewer 128-query blocks than half the CUs merge
+ * blocks split over two workgroups through a fixed context buffer (~9 MB on
+ * 256 CUs), allocated by the first such call outside capture; during capture
+ * before then, the call takes another schedule instead. Switching streams
+ * (wrs_attn_set_stream) drains the old stream unless either stream is
+ * recording a graph. Zero fields are ignored; reserving never shrinks.
+ * Synchronous. */
 typedef struct wrs_reserve {
     size_t n_heads;        /* heads of the planes decode and capture read */
     size_t decode_rows;    /* query rows of one decode call: slots or beams */

@@ -153,3 +153,51 @@ def test_scratch_growth_during_capture_is_refused(wrs, fresh_ctx):
     assert np.isfinite(host(out_c)).all() and maxerr(host(out_c), ref) < 10
     cross.close()
     selfa.close()
+
+
+def test_split_prefill_under_graph_capture(wrs, fresh_ctx):
+    # One whisper-base window (96 blocks of 128 queries, fewer than half the
+    # CUs) splits each block over two workgroups through context scratch that
+    # the first call outside capture allocates. Captured before that call,
+    # the prefill takes the key split instead (no allocation, no error);
+    # captured after it, the split blocks replay bit-identically to eager
+    # calls, with eager work between the replays.
+    from wrs_amd import workloads as W
+    note("16-bit prefill of one whisper-base window under graph capture")
+    ctx = fresh_ctx
+    H, T = 8, 1500
+    x = [dev(W.normal((T, H * 64), 40 + i, storage="f16"), torch.float16) for i in range(3)]
+    lay = wrs.token_major(T, H * 64, 64)
+    out = torch.zeros((T, H * 64), device="cuda")
+
+    def run():
+        wrs.prefill(x[0], x[1], x[2], out, batch=1, n_heads=H, t_q=T, t_kv=T, d_head=64,
+                    q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g0):
+        ctx.use_torch_stream()
+        run()
+    ctx.use_torch_stream()
+    out.fill_(float("nan"))
+    g0.replay()
+    torch.cuda.synchronize()
+    before = out.clone()
+    run()  # outside capture: allocates the scratch, runs the split blocks
+    torch.cuda.synchronize()
+    ref = out.clone()
+    assert torch.isfinite(ref).all()
+    assert maxerr(host(before), host(ref)) < 1e-4, "key split and split blocks disagree"
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        ctx.use_torch_stream()
+        run()
+    ctx.use_torch_stream()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        g1.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}: split prefill differs from eager"
+        run()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"eager call after replay {rep} differs"

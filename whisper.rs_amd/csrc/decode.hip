@@ -83,12 +83,6 @@ __device__ inline float wave_sum(float x) {
   return x + __shfl_xor(x, 32);
 }
 
-__device__ inline void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float ld_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 __device__ inline float pow2(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
 

@@ -77,6 +77,11 @@ constexpr int kTileH = kN * 64;     // 16-bit elements per K (or V) tile: 8 KiB
 constexpr int kRowsPerWave = kN / kWaves;  // tile rows one wave copies
 constexpr int kRowGroups = kRowsPerWave / 8;  // one 1 KiB DMA per 8 rows
 constexpr int kDmaPerTile = 2 * kRowGroups;   // K and V
+// Split blocks: floats one wave publishes (32 O registers, max and sum, each
+// for 64 lanes), and words between merge counters (one 128-byte line each).
+constexpr int kSplitPartWave = 34 * 64;
+constexpr int kSplitCounterStride = 32;
+constexpr int kSplitWays = 2;  // workgroups per split block
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSumLimit = 16384.0f;  // row sum of one step that forces a rescale
 constexpr float kNoMax = -1.0e30f;     // reference max before the first step
@@ -246,10 +251,12 @@ static_assert(pipe_order_ok<1>() && pipe_order_ok<2>(), "pipelined step order");
 // waves (three with QW = 6) on every SIMD of the CUs in use instead of one.
 // With QW = 6 the first four waves of a half move its tiles and the other
 // two only compute.
-template <typename T, int QB, int KH, int QW = kWaves>
+template <typename T, int QB, int KH, int QW = kWaves, int WS = 1>
 __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     PrefillArgs a, int n_qblk) {
   static_assert(KH == 1 || KH == 2, "one or two key halves");
+  static_assert(WS == 1 || (WS == 2 && KH == 2 && QB == 1 && QW == kWaves),
+                "blocks split over two workgroups: 128 queries, key halves");
   static_assert(QW == kWaves || (QW == 6 && QB == 1 && KH == 2),
                 "six query waves: one block each, key halves");
   constexpr int kQB = QB;
@@ -259,11 +266,15 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
   __shared__ __attribute__((aligned(128))) uint16_t Ks[KH * kNB * kTileH];
   __shared__ __attribute__((aligned(128))) uint16_t Vs[KH * kNB * kTileH];
   __shared__ int nonfinite;  // bf16: some output of the workgroup is inf/NaN
+  __shared__ int merger;     // split blocks: this workgroup merges the block
   static_assert(sizeof(f32blk::Tiles<2>) <= sizeof(Ks), "f32 tiles fit in the K buffers");
 
   const int lid = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
-  const int qblk = lid % n_qblk;
-  const int bh = lid / n_qblk;
+  // Split blocks: the block's WS workgroups are neighbours in lid (one XCD).
+  const int wsplit = WS == 1 ? 0 : lid % WS;
+  const int blk = WS == 1 ? lid : lid / WS;  // (window, head, query block)
+  const int qblk = blk % n_qblk;
+  const int bh = blk / n_qblk;
   const int h = bh % a.n_heads;
   const int b = bh / a.n_heads;
 
@@ -308,13 +319,16 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     kv_end = min(kv_end, last + 1);
   }
   const int n_tiles_all = (kv_end + kN - 1) / kN;
-  // This half's tiles (local tile t is tile KH t + half of the block's keys)
-  // and the most that any half has.
-  const int n_tiles = (n_tiles_all - half + KH - 1) / KH;
-  const int t_most = (n_tiles_all + KH - 1) / KH;
+  // The block's tiles fall into kP parts taken in turn (key halves, over WS
+  // workgroups): this half's part, its tiles (local tile t is tile kP t + part
+  // of the block's keys) and the most that a half of this workgroup has.
+  constexpr int kP = KH * WS;
+  const int part = KH * wsplit + half;
+  const int n_tiles = (n_tiles_all - part + kP - 1) / kP;
+  const int t_most = (n_tiles_all - KH * wsplit + kP - 1) / kP;
   const int nh = 2 * n_tiles;  // this half's 32-key steps
   // The block's 32-key step of this half's step j.
-  auto gstep = [&](int j) { return 2 * (KH * (j >> 1) + half) + (j & 1); };
+  auto gstep = [&](int j) { return 2 * (kP * (j >> 1) + part) + (j & 1); };
   // First step that needs a mask: keys past t_kv, or (causal) past the first
   // query of the workgroup.
   int first_masked = a.t_kv / 32;
@@ -341,10 +355,10 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     const uint32_t buf = __builtin_amdgcn_readfirstlane((t % kNB) * (kTileH * 2));
 #pragma unroll
     for (int r = 0; r < kRowGroups; ++r)
-      dma16(krs, ks_lds + buf + 1024 * r, kofs[r] + (KH * t + half) * kstep);
+      dma16(krs, ks_lds + buf + 1024 * r, kofs[r] + (kP * t + part) * kstep);
 #pragma unroll
     for (int r = 0; r < kRowGroups; ++r)
-      dma16(vrs, vs_lds + buf + 1024 * r, vofs[r] + (KH * t + half) * vstep);
+      dma16(vrs, vs_lds + buf + 1024 * r, vofs[r] + (kP * t + part) * vstep);
   };
   // bf16 V -> f16 in place: this wave's own rows, whose loads have landed.
   auto convert_tile = [&](int t) {
@@ -681,7 +695,7 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     };
     // Tile 0 (no PV yet), full tiles (both steps complete and unmasked), then
     // the tail.
-    const int t_full_end = min(n_tiles - 1, (first_masked / 2 - half + KH - 1) / KH);
+    const int t_full_end = min(n_tiles - 1, (first_masked / 2 - part + kP - 1) / kP);
     tile(Part{}, 0);
     int t = 1;
     for (; t < t_full_end; ++t) tile(Full{}, t);
@@ -735,6 +749,61 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     // The output staging below reaches into half 1's K ring, where the max and
     // sum were, when it needs more than half 0's.
     if constexpr (QW * 32 * kQB * 256 > kNB * kTileH * 2) __syncthreads();
+  }
+  if constexpr (WS > 1) {
+    // The block's workgroups each publish half 0's (O, max, sum), lane by
+    // lane, as agent-scope stores; after every wave has waited for its stores,
+    // one thread counts the workgroup in. The workgroup that counts last
+    // folds the partials (log-sum-exp, exp2 domain), re-arms the counter and
+    // writes the output; the others are done. The fold takes the partials in
+    // split order whichever workgroup runs it, so the bits do not depend on
+    // which one finishes last.
+    constexpr int kPart = kWaves * kSplitPartWave;
+    if (half == 0) {
+      float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + wsplit) * kPart +
+                       wq * kSplitPartWave + lane;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st_agent(p + (16 * hf + i) * 64, o[0][hf][i]);
+      st_agent(p + 32 * 64, m[0]);
+      st_agent(p + 33 * 64, l[0]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned* const counter = a.split_counters + static_cast<int64_t>(blk) * kSplitCounterStride;
+    if (tid == 0)
+      merger = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               static_cast<unsigned>(WS - 1);
+    __syncthreads();
+    if (!merger) return;
+    static_assert(WS == 2, "the fold below takes two partials");
+    if (half == 0) {
+      const float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + (1 - wsplit)) * kPart +
+                             wq * kSplitPartWave + lane;
+      float ox[2][16];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ox[hf][i] = ld_agent(p + (16 * hf + i) * 64);
+      const float mx = ld_agent(p + 32 * 64), lx = ld_agent(p + 33 * 64);
+      // Split 0's partial is (m0, l0, O0) and split 1's (m1, l1, O1).
+      const bool own0 = wsplit == 0;
+      const float m0 = own0 ? m[0] : mx, m1 = own0 ? mx : m[0];
+      const float l0 = own0 ? l[0] : lx, l1 = own0 ? lx : l[0];
+      const float mm = fmaxf(m0, m1);
+      const float e0 = __builtin_amdgcn_exp2f(m0 - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
+      l[0] = l0 * e0 + l1 * e1;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float o0 = own0 ? o[0][hf][i] : ox[hf][i], o1 = own0 ? ox[hf][i] : o[0][hf][i];
+          o[0][hf][i] = o0 * e0 + o1 * e1;
+        }
+      m[0] = mm;
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // The outputs leave as whole 256-byte query rows. Each wave stages its
@@ -1185,17 +1254,17 @@ int64_t device_cus() {
   return cus;
 }
 
-template <int QB, int KH, int QW = kWaves>
+template <int QB, int KH, int QW = kWaves, int WS = 1>
 hipError_t launch_qb(const PrefillArgs& a, DType dt, hipStream_t s) {
   constexpr int kM = queries_per_wg<QB, QW>();
   const int n_qblk = (a.t_q + kM - 1) / kM;
-  const int64_t nwg = n_qblk * static_cast<int64_t>(a.n_heads) * a.batch;
+  const int64_t nwg = n_qblk * static_cast<int64_t>(a.n_heads) * a.batch * WS;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(nwg)), block(64 * QW * KH);
   if (dt == kF16)
-    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB, KH, QW>), grid, block, 0, s, a, n_qblk);
+    hipLaunchKernelGGL((fa2_prefill_d64<_Float16, QB, KH, QW, WS>), grid, block, 0, s, a, n_qblk);
   else
-    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB, KH, QW>), grid, block, 0, s, a, n_qblk);
+    hipLaunchKernelGGL((fa2_prefill_d64<__bf16, QB, KH, QW, WS>), grid, block, 0, s, a, n_qblk);
   return hipGetLastError();
 }
 
@@ -1209,6 +1278,46 @@ bool prefill_mfma16_supports(const PrefillArgs& a) {
   return a.d_head == 64 && a.lk.rs >= 64 && a.lv.rs >= 64 && span_k < (int64_t{1} << 31) &&
          span_v < (int64_t{1} << 31);
 }
+
+namespace {
+
+// Scratch of a grid of nwg1 split 128-query blocks.
+int64_t split_floats(int64_t nwg1) { return nwg1 * kSplitWays * kWaves * kSplitPartWave; }
+int64_t split_words(int64_t nwg1) { return nwg1 * kSplitCounterStride; }
+
+bool split_fits(const PrefillArgs& a, int64_t nwg1) {
+  return a.split_part && a.split_counters &&
+         split_floats(nwg1) <= static_cast<int64_t>(a.split_part_floats) &&
+         split_words(nwg1) <= static_cast<int64_t>(a.split_counter_words);
+}
+
+// Does the schedule split each 128-query block over two workgroups? By
+// default for grids of fewer 128-query blocks than half the CUs (which then
+// run two workgroups of 8 waves per block) over at least 1024 keys: one
+// whisper-tiny or -base window, 72 or 96 blocks, 14.9 against 18.2 us with
+// the key split. Over fewer keys the merge through memory costs more than it
+// saves (448 keys, 24 blocks: 9.8 against 7.2 us).
+bool split_schedule(const PrefillArgs& a, int64_t nwg1, int64_t cus) {
+  return a.force_queries == -64 ||
+         (a.force_queries == 0 && 2 * nwg1 < cus && a.t_kv >= 1024);
+}
+
+int64_t blocks128(const PrefillArgs& a) {
+  constexpr int kM1 = queries_per_wg<1>();
+  return ((a.t_q + kM1 - 1) / kM1) * static_cast<int64_t>(a.n_heads) * a.batch;
+}
+
+}  // namespace
+
+void prefill_mfma16_scratch(const PrefillArgs& a, size_t* part_floats, size_t* counter_words) {
+  const int64_t nwg1 = blocks128(a);
+  const bool used = a.t_q > 0 && nwg1 > 0 && split_schedule(a, nwg1, device_cus());
+  *part_floats = used ? static_cast<size_t>(split_floats(nwg1)) : 0;
+  *counter_words = used ? static_cast<size_t>(split_words(nwg1)) : 0;
+}
+
+size_t prefill_split_floats_min() { return static_cast<size_t>(split_floats(device_cus() / 2)); }
+size_t prefill_split_words_min() { return static_cast<size_t>(split_words(device_cus() / 2)); }
 
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) {
   if (!prefill_mfma16_supports(a)) return hipErrorInvalidValue;
@@ -1229,15 +1338,17 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   // - half the CUs <= n <= 1 per CU: 128-query blocks on 8-wave workgroups
   //   with key halves (one large-v3 window, 240 blocks: 21.5 against 25.7 us;
   //   one whisper-small window, 144 blocks: 18.6 against 21.4);
-  // - fewer: the key split (32-query workgroups), which spreads a block over
-  //   four CUs (one whisper-tiny window, 72 blocks: 18.3 against 18.4 us with
-  //   key halves). It streams a block's K/V per 32 queries, 4x the bytes per
-  //   FLOP of the 128-query kernel, which caps it near 50 GB/s per CU.
+  // - fewer, over at least 1024 keys: each block on two such workgroups,
+  //   each over half its keys, merged through memory (split_schedule);
+  // - fewer otherwise: the key split (32-query workgroups), which spreads a
+  //   block over four CUs. It streams a block's K/V per 32 queries, 4x the
+  //   bytes per FLOP of the 128-query kernel, which caps it near 50 GB/s per
+  //   CU.
   // Below two blocks per CU a launch is one round of workgroups (~20-30 us),
   // in which each workgroup's fixed costs (q and the first tiles, the output
   // rows) are not hidden. a.force_queries forces one schedule: 256 or 128
   // queries per 4-wave workgroup, -256, -192 or -128 that many on 8 or 12
-  // waves with key halves, 32 the key split.
+  // waves with key halves, -64 the split blocks, 32 the key split.
   constexpr int kM1 = queries_per_wg<1>();
   constexpr int kM6 = queries_per_wg<1, 6>();
   const int64_t nwg1 = ((a.t_q + kM1 - 1) / kM1) * bh;
@@ -1251,6 +1362,12 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
     return launch_qb<2, 2>(a, dt, s);
   if (a.force_queries == 128 || (by_grid && nwg1 > cus)) return launch_qb<1, 1>(a, dt, s);
   if (a.force_queries == -128 || (by_grid && 2 * nwg1 >= cus)) return launch_qb<1, 2>(a, dt, s);
+  if (split_schedule(a, nwg1, cus)) {
+    if (split_fits(a, nwg1)) return launch_qb<1, 2, kWaves, kSplitWays>(a, dt, s);
+    // No scratch (a call under stream capture before any outside it): the
+    // key split below, unless forced.
+    if (a.force_queries == -64) return hipErrorInvalidValue;
+  }
   const int n_qblk = (a.t_q + kKsQ - 1) / kKsQ;
   const int64_t nwg = n_qblk * bh;
   if (nwg > 0x7fffffff) return hipErrorInvalidConfiguration;

@@ -50,6 +50,14 @@ struct wrs_attn_ctx {
   size_t ln_x_bytes = 0;
   float* exact_scores = nullptr;  // f32 arena attention: full score rows
   size_t exact_scores_bytes = 0;
+  // 16-bit prefill blocks whose keys split over two workgroups: partials and
+  // merge counters (kept zero between launches). Allocated at their first use
+  // for at least kSplitScratchBlocks blocks, so that every grid the default
+  // schedule splits fits and graphs captured later keep valid pointers.
+  float* split_part = nullptr;
+  size_t split_part_bytes = 0;
+  unsigned* split_counters = nullptr;
+  size_t split_counter_bytes = 0;
   // Prefill schedule overrides (wrs_attn_set_schedule).
   int prefill_queries = 0;
   int f32_split = -1;
@@ -266,6 +274,24 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
   };
   if (same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
       aligned16(v, lv, 8) && aligned16(out, lo, 4) && wrs::prefill_mfma16_supports(a)) {
+    // Scratch for a schedule that splits blocks over workgroups. Outside
+    // capture it is allocated (or, for a forced schedule on a larger grid,
+    // grown) here; during capture the kernel takes another schedule when what
+    // exists does not fit.
+    size_t pf = 0, cw = 0;
+    wrs::prefill_mfma16_scratch(a, &pf, &cw);
+    if (pf && !capturing(c)) {
+      int rc = grow(c, reinterpret_cast<void**>(&c->split_part), &c->split_part_bytes,
+                    std::max(pf, wrs::prefill_split_floats_min()) * sizeof(float), false);
+      if (rc) return rc;
+      rc = grow(c, reinterpret_cast<void**>(&c->split_counters), &c->split_counter_bytes,
+                std::max(cw, wrs::prefill_split_words_min()) * sizeof(unsigned), true);
+      if (rc) return rc;
+    }
+    a.split_part = c->split_part;
+    a.split_part_floats = c->split_part_bytes / sizeof(float);
+    a.split_counters = c->split_counters;
+    a.split_counter_words = c->split_counter_bytes / sizeof(unsigned);
     WRS_HIP(c, wrs::launch_prefill_mfma16(a, q_dtype == WRS_F16 ? wrs::kF16 : wrs::kBF16,
                                           c->stream));
     return WRS_OK;
@@ -475,6 +501,8 @@ void wrs_attn_destroy(wrs_attn_ctx* c) {
   if (c->lin_x) (void)hipFree(c->lin_x);
   if (c->ln_x) (void)hipFree(c->ln_x);
   if (c->exact_scores) (void)hipFree(c->exact_scores);
+  if (c->split_part) (void)hipFree(c->split_part);
+  if (c->split_counters) (void)hipFree(c->split_counters);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   noalloc_release(c);  // the stream is drained: no call uses the slot any more
   delete c;
@@ -506,9 +534,10 @@ int wrs_attn_set_schedule(wrs_attn_ctx* c, int prefill_queries, int f32_split) {
   if (!c) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
   if (prefill_queries != 0 && prefill_queries != 32 && prefill_queries != 128 &&
-      prefill_queries != 256 && prefill_queries != -128 && prefill_queries != -192 &&
-      prefill_queries != -256)
-    return fail(c, WRS_EINVAL, "prefill_queries must be 0, 32, 128, 256, -128, -192 or -256");
+      prefill_queries != 256 && prefill_queries != -64 && prefill_queries != -128 &&
+      prefill_queries != -192 && prefill_queries != -256)
+    return fail(c, WRS_EINVAL,
+                "prefill_queries must be 0, 32, 128, 256, -64, -128, -192 or -256");
   if (f32_split < -1 || f32_split > 4)
     return fail(c, WRS_EINVAL, "f32_split must be -1..4");
   c->prefill_queries = prefill_queries;

@@ -36,6 +36,15 @@ struct Layout {
 
 // Flash-attention prefill over full query/key sequences
 // (crates/tensor/src/ops/attention.rs:68-243 semantics).
+// Agent-scope (L2-coherent across the GPU's XCDs) store and load of one
+// float, for partials that another workgroup of the launch merges.
+__device__ inline void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct PrefillArgs {
   const void* q;
   const void* k;
@@ -52,11 +61,25 @@ struct PrefillArgs {
   // 2..4 = that many waves).
   int force_queries;
   int force_f32_split;
+  // Context scratch for 16-bit grids whose blocks split their keys over two
+  // workgroups (null when none is available): partials and merge counters
+  // (zero between launches), with their sizes.
+  float* split_part;
+  size_t split_part_floats;
+  unsigned* split_counters;
+  size_t split_counter_words;
 };
 
 // MFMA f16/bf16 kernel, d_head == 64, q/k/v of one 16-bit type, rows 16-byte
 // aligned; prefill_mfma16_supports() states the remaining shape limits.
 bool prefill_mfma16_supports(const PrefillArgs& a);
+// Scratch the 16-bit kernel's schedule for `a` uses (floats of partials and
+// words of counters), both 0 when it uses none.
+void prefill_mfma16_scratch(const PrefillArgs& a, size_t* part_floats, size_t* counter_words);
+// The sizes the context allocates at least: enough for every grid whose
+// blocks the default schedule splits over workgroups.
+size_t prefill_split_floats_min();
+size_t prefill_split_words_min();
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s);
 // f32-accumulate-check kernel on f32 MFMA: q f32, k/v f32|f16|bf16 widened
 // exactly to f32, any d_head <= 128.
