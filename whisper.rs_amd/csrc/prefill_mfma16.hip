@@ -77,9 +77,10 @@ constexpr int kTileH = kN * 64;     // 16-bit elements per K (or V) tile: 8 KiB
 constexpr int kRowsPerWave = kN / kWaves;  // tile rows one wave copies
 constexpr int kRowGroups = kRowsPerWave / 8;  // one 1 KiB DMA per 8 rows
 constexpr int kDmaPerTile = 2 * kRowGroups;   // K and V
-// Split blocks: floats one wave publishes (32 O registers, max and sum, each
-// for 64 lanes), and words between merge counters (one 128-byte line each).
-constexpr int kSplitPartWave = 34 * 64;
+// Split blocks: floats one wave publishes (its 16 O registers, max and sum,
+// each for 64 lanes), and words between merge counters (one 128-byte line
+// each).
+constexpr int kSplitPartWave = 18 * 64;
 constexpr int kSplitCounterStride = 32;
 constexpr int kSplitWays = 2;  // workgroups per split block
 constexpr float kLog2e = 1.4426950408889634f;
@@ -708,66 +709,80 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     const int mine = n_tiles > 0 ? 1 + n_tiles : 0;
     const int most = t_most > 0 ? 1 + t_most : 0;
     for (int i = mine; i < most; ++i) tile_barrier();
-    // No wave reads a tile any more and every tile load has landed: half 1
-    // leaves its O (in the V rings, as [wave][block][register][lane]) and its
-    // max and sum (in its K ring), and half 0 folds them into its own by the
-    // log-sum-exp rule (exp2 domain). A half without keys holds the initial
-    // max and zero sums.
-    float* const xo = reinterpret_cast<float*>(Vs);
-    float* const xm = reinterpret_cast<float*>(Ks + kNB * kTileH);
-    static_assert(QW * kQB * 32 * 64 * 4 <= static_cast<int>(sizeof(Vs)), "O fits");
-    static_assert(QW * kQB * 2 * 64 * 4 <= kNB * kTileH * 2, "max and sum fit");
-    if (half == 1) {
+    // No wave reads a tile any more and every tile load has landed. Half h
+    // keeps, and will write, the 32 output columns of its accumulator block h
+    // (d 32h..32h+31): it leaves the other block of its O in its own V ring
+    // and its max and sum in its own K ring ([wave][block][register][lane]),
+    // and after a barrier folds the other half's values for its block into
+    // its own by the log-sum-exp rule (exp2 domain), taking the halves in
+    // order, so both compute the same sums. A half without keys holds the
+    // initial max and zero sums.
+    constexpr int kRing = kNB * kTileH;  // 16-bit elements of one half's K or V ring
+    static_assert(QW * kQB * 16 * 64 * 4 <= kRing * 2, "O block fits a ring");
+    static_assert(QW * kQB * 2 * 64 * 4 <= kRing * 2, "max and sum fit a ring");
+    float* const xo_mine = reinterpret_cast<float*>(Vs + half * kRing);
+    float* const xm_mine = reinterpret_cast<float*>(Ks + half * kRing);
+    const float* const xo_other = reinterpret_cast<const float*>(Vs + (1 - half) * kRing);
+    const float* const xm_other = reinterpret_cast<const float*>(Ks + (1 - half) * kRing);
 #pragma unroll
-      for (int j = 0; j < kQB; ++j) {
+    for (int j = 0; j < kQB; ++j) {
+      float* const po = xo_mine + (wq * kQB + j) * 16 * 64 + lane;
+      if (half == 0) {
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+        for (int i = 0; i < 16; ++i) po[i * 64] = o[j][1][i];
+      } else {
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            xo[((wq * kQB + j) * 32 + 16 * hf + i) * 64 + lane] = o[j][hf][i];
-        xm[((wq * kQB + j) * 2) * 64 + lane] = m[j];
-        xm[((wq * kQB + j) * 2 + 1) * 64 + lane] = l[j];
+        for (int i = 0; i < 16; ++i) po[i * 64] = o[j][0][i];
       }
+      xm_mine[((wq * kQB + j) * 2) * 64 + lane] = m[j];
+      xm_mine[((wq * kQB + j) * 2 + 1) * 64 + lane] = l[j];
     }
     __syncthreads();
-    if (half == 0) {
 #pragma unroll
-      for (int j = 0; j < kQB; ++j) {
-        const float m1 = xm[((wq * kQB + j) * 2) * 64 + lane];
-        const float l1 = xm[((wq * kQB + j) * 2 + 1) * 64 + lane];
-        const float mm = fmaxf(m[j], m1);
-        const float e0 = __builtin_amdgcn_exp2f(m[j] - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
-        l[j] = l[j] * e0 + l1 * e1;
+    for (int j = 0; j < kQB; ++j) {
+      const float mx = xm_other[((wq * kQB + j) * 2) * 64 + lane];
+      const float lx = xm_other[((wq * kQB + j) * 2 + 1) * 64 + lane];
+      const float m0 = half == 0 ? m[j] : mx, m1 = half == 0 ? mx : m[j];
+      const float l0 = half == 0 ? l[j] : lx, l1 = half == 0 ? lx : l[j];
+      const float mm = fmaxf(m0, m1);
+      const float e0 = __builtin_amdgcn_exp2f(m0 - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
+      l[j] = l0 * e0 + l1 * e1;
+      const float* const px = xo_other + (wq * kQB + j) * 16 * 64 + lane;
+      if (half == 0) {
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+        for (int i = 0; i < 16; ++i) o[j][0][i] = o[j][0][i] * e0 + px[i * 64] * e1;
+      } else {
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            o[j][hf][i] = o[j][hf][i] * e0 + xo[((wq * kQB + j) * 32 + 16 * hf + i) * 64 + lane] * e1;
-        m[j] = mm;
+        for (int i = 0; i < 16; ++i) o[j][1][i] = px[i * 64] * e0 + o[j][1][i] * e1;
       }
+      m[j] = mm;
     }
-    // The output staging below reaches into half 1's K ring, where the max and
-    // sum were, when it needs more than half 0's.
-    if constexpr (QW * 32 * kQB * 256 > kNB * kTileH * 2) __syncthreads();
+    // The output staging below reuses the rings.
+    __syncthreads();
   }
   if constexpr (WS > 1) {
-    // The block's workgroups each publish half 0's (O, max, sum), lane by
-    // lane, as agent-scope stores; after every wave has waited for its stores,
-    // one thread counts the workgroup in. The workgroup that counts last
-    // folds the partials (log-sum-exp, exp2 domain), re-arms the counter and
-    // writes the output; the others are done. The fold takes the partials in
-    // split order whichever workgroup runs it, so the bits do not depend on
-    // which one finishes last.
-    constexpr int kPart = kWaves * kSplitPartWave;
-    if (half == 0) {
-      float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + wsplit) * kPart +
-                       wq * kSplitPartWave + lane;
+    // The block's workgroups each publish every wave's (O block, max, sum),
+    // lane by lane, as agent-scope stores; after every wave has waited for
+    // its stores, one thread counts the workgroup in. The workgroup that
+    // counts last folds the partials (log-sum-exp, exp2 domain), re-arms the
+    // counter and writes the output; the others are done. The fold takes the
+    // partials in split order whichever workgroup runs it, so the bits do not
+    // depend on which one finishes last.
+    static_assert(WS == 2 && kQB == 1, "the fold below takes two partials of one block");
+    constexpr int kPart = KH * kWaves * kSplitPartWave;
+    const int pw = (half * kWaves + wq) * kSplitPartWave + lane;
+    {
+      float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + wsplit) * kPart + pw;
+      auto publish = [&](const f32x16& ob) __attribute__((always_inline)) {
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st_agent(p + (16 * hf + i) * 64, o[0][hf][i]);
-      st_agent(p + 32 * 64, m[0]);
-      st_agent(p + 33 * 64, l[0]);
+        for (int i = 0; i < 16; ++i) st_agent(p + i * 64, ob[i]);
+      };
+      if (half == 0)
+        publish(o[0][0]);
+      else
+        publish(o[0][1]);
+      st_agent(p + 16 * 64, m[0]);
+      st_agent(p + 17 * 64, l[0]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -777,16 +792,13 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
                static_cast<unsigned>(WS - 1);
     __syncthreads();
     if (!merger) return;
-    static_assert(WS == 2, "the fold below takes two partials");
-    if (half == 0) {
-      const float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + (1 - wsplit)) * kPart +
-                             wq * kSplitPartWave + lane;
-      float ox[2][16];
+    {
+      const float* const p =
+          a.split_part + (static_cast<int64_t>(blk) * WS + (1 - wsplit)) * kPart + pw;
+      float ox[16];
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ox[hf][i] = ld_agent(p + (16 * hf + i) * 64);
-      const float mx = ld_agent(p + 32 * 64), lx = ld_agent(p + 33 * 64);
+      for (int i = 0; i < 16; ++i) ox[i] = ld_agent(p + i * 64);
+      const float mx = ld_agent(p + 16 * 64), lx = ld_agent(p + 17 * 64);
       // Split 0's partial is (m0, l0, O0) and split 1's (m1, l1, O1).
       const bool own0 = wsplit == 0;
       const float m0 = own0 ? m[0] : mx, m1 = own0 ? mx : m[0];
@@ -794,62 +806,65 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
       const float mm = fmaxf(m0, m1);
       const float e0 = __builtin_amdgcn_exp2f(m0 - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
       l[0] = l0 * e0 + l1 * e1;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+      auto fold = [&](f32x16& ob) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float o0 = own0 ? o[0][hf][i] : ox[hf][i], o1 = own0 ? ox[hf][i] : o[0][hf][i];
-          o[0][hf][i] = o0 * e0 + o1 * e1;
+          const float o0 = own0 ? ob[i] : ox[i], o1 = own0 ? ox[i] : ob[i];
+          ob[i] = o0 * e0 + o1 * e1;
         }
+      };
+      if (half == 0)
+        fold(o[0][0]);
+      else
+        fold(o[0][1]);
       m[0] = mm;
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  // The outputs leave as whole 256-byte query rows. Each wave stages its
-  // 32*QB rows in the LDS tiles (no longer read after the last tile barrier,
-  // and every tile load has landed), 16-byte chunk c of row r at c ^ (r % 16),
-  // then 16 lanes store one row: stored straight from the MFMA layout, one
-  // instruction would write 32 bytes to each of 32 rows.
-  constexpr int kStageBytes = 32 * kQB * 256;
-  static_assert(QW * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
-  // (With key halves, half 0's waves store: their rows fit in the K rings.)
-  char* const stage = wq * kStageBytes < static_cast<int>(sizeof(Ks))
-                          ? reinterpret_cast<char*>(Ks) + wq * kStageBytes
-                          : reinterpret_cast<char*>(Vs) + (wq * kStageBytes - sizeof(Ks));
   // Sum of this lane's outputs: inf/NaN when any of them is.
   float chk = 0.f;
-  if (half == 0) {
+  // The wave's first query.
+  const int qw = qblk * kM + wq * (32 * kQB);
+  if constexpr (KH == 1) {
+    // The outputs leave as whole 256-byte query rows. Each wave stages its
+    // 32*QB rows in the LDS tiles (no longer read after the last tile
+    // barrier, and every tile load has landed), 16-byte chunk c of row r at
+    // c ^ (r % 16), then 16 lanes store one row: stored straight from the
+    // MFMA layout, one instruction would write 32 bytes to each of 32 rows.
+    constexpr int kStageBytes = 32 * kQB * 256;
+    static_assert(QW * kStageBytes <= static_cast<int>(sizeof(Ks) + sizeof(Vs)), "staging fits");
+    char* const stage = wq * kStageBytes < static_cast<int>(sizeof(Ks))
+                            ? reinterpret_cast<char*>(Ks) + wq * kStageBytes
+                            : reinterpret_cast<char*>(Vs) + (wq * kStageBytes - sizeof(Ks));
 #pragma unroll
-  for (int j = 0; j < kQB; ++j) {
-    // l is the whole row sum in both lanes of the query (the row sums are).
-    const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
-    const int rr = 32 * j + r32;  // row within the wave's block
-    char* const srow = stage + rr * 256;
+    for (int j = 0; j < kQB; ++j) {
+      // l is the whole row sum in both lanes of the query (the row sums are).
+      const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
+      const int rr = 32 * j + r32;  // row within the wave's block
+      char* const srow = stage + rr * 256;
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4 lo4 =
-          f32x4{o[j][0][4 * gq], o[j][0][4 * gq + 1], o[j][0][4 * gq + 2], o[j][0][4 * gq + 3]} *
-          inv;
-      const f32x4 hi4 =
-          f32x4{o[j][1][4 * gq], o[j][1][4 * gq + 1], o[j][1][4 * gq + 2], o[j][1][4 * gq + 3]} *
-          inv;
-      *reinterpret_cast<f32x4*>(srow + (((2 * gq + hl) ^ (rr & 15)) * 16)) = lo4;
-      *reinterpret_cast<f32x4*>(srow + (((8 + 2 * gq + hl) ^ (rr & 15)) * 16)) = hi4;
-      if constexpr (Elem<T>::kConvertV) {
-        if (q0 + 32 * j < a.t_q)
-          chk += (lo4[0] + lo4[1]) + (lo4[2] + lo4[3]) + (hi4[0] + hi4[1]) + (hi4[2] + hi4[3]);
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4 lo4 =
+            f32x4{o[j][0][4 * gq], o[j][0][4 * gq + 1], o[j][0][4 * gq + 2], o[j][0][4 * gq + 3]} *
+            inv;
+        const f32x4 hi4 =
+            f32x4{o[j][1][4 * gq], o[j][1][4 * gq + 1], o[j][1][4 * gq + 2], o[j][1][4 * gq + 3]} *
+            inv;
+        *reinterpret_cast<f32x4*>(srow + (((2 * gq + hl) ^ (rr & 15)) * 16)) = lo4;
+        *reinterpret_cast<f32x4*>(srow + (((8 + 2 * gq + hl) ^ (rr & 15)) * 16)) = hi4;
+        if constexpr (Elem<T>::kConvertV) {
+          if (q0 + 32 * j < a.t_q)
+            chk += (lo4[0] + lo4[1]) + (lo4[2] + lo4[3]) + (hi4[0] + hi4[1]) + (hi4[2] + hi4[3]);
+        }
       }
     }
-  }
-  // The wave reads back what its own lanes wrote: LDS operations of one wave
-  // complete in order.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  {
+    // The wave reads back what its own lanes wrote: LDS operations of one
+    // wave complete in order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int c16 = lane & 15;
-    const int qw = qblk * kM + wq * (32 * kQB);  // the wave's first query
     float* const ob = a.o + b * a.lo.bs + h * a.lo.hs + 4 * c16;
 #pragma unroll
     for (int k = 0; k < 8 * kQB; ++k) {
@@ -861,8 +876,50 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
       if (qw + rr < a.t_q)
         __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(qw + rr) * a.lo.rs));
     }
+  } else {
+    // Key halves: half h writes columns d 32h..32h+31 of its waves' rows as
+    // 128-byte half rows, staged in its own K ring with 16-byte chunk c of
+    // row r at c ^ ((r / 2) % 8) (a 16-lane phase of the writes covers 16
+    // rows, two per 256-byte bank line, and of the reads two whole rows),
+    // then 8 lanes store one half row.
+    constexpr int kStageBytes = 32 * kQB * 128;
+    static_assert(QW * kStageBytes <= kNB * kTileH * 2, "a half's rows fit its K ring");
+    char* const stage = reinterpret_cast<char*>(Ks + half * (kNB * kTileH)) + wq * kStageBytes;
+    auto put = [&](const f32x16& ov, int j) __attribute__((always_inline)) {
+      const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
+      const int rr = 32 * j + r32;
+      char* const srow = stage + rr * 128;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4 v4 =
+            f32x4{ov[4 * gq], ov[4 * gq + 1], ov[4 * gq + 2], ov[4 * gq + 3]} * inv;
+        *reinterpret_cast<f32x4*>(srow + (((2 * gq + hl) ^ ((rr >> 1) & 7)) * 16)) = v4;
+        if constexpr (Elem<T>::kConvertV) {
+          if (q0 + 32 * j < a.t_q) chk += (v4[0] + v4[1]) + (v4[2] + v4[3]);
+        }
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) {
+      if (half == 0)
+        put(o[j][0], j);
+      else
+        put(o[j][1], j);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int c8 = lane & 7;
+    float* const ob = a.o + b * a.lo.bs + h * a.lo.hs + 32 * half + 4 * c8;
+#pragma unroll
+    for (int k = 0; k < 4 * kQB; ++k) {
+      const int rr = 8 * k + (lane >> 3);
+      const f32x4 v =
+          *reinterpret_cast<const f32x4*>(stage + rr * 128 + ((c8 ^ ((rr >> 1) & 7)) * 16));
+      if (qw + rr < a.t_q)
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(ob + static_cast<int64_t>(qw + rr) * a.lo.rs));
+    }
   }
-  }  // half 0
   if constexpr (Elem<T>::kConvertV) {
     // A bf16 V value of magnitude >= 65536 is inf after the f16 conversion and
     // turns the rows that meet it into inf/NaN (a finite sum that overflows
@@ -1282,7 +1339,7 @@ bool prefill_mfma16_supports(const PrefillArgs& a) {
 namespace {
 
 // Scratch of a grid of nwg1 split 128-query blocks.
-int64_t split_floats(int64_t nwg1) { return nwg1 * kSplitWays * kWaves * kSplitPartWave; }
+int64_t split_floats(int64_t nwg1) { return nwg1 * kSplitWays * 2 * kWaves * kSplitPartWave; }
 int64_t split_words(int64_t nwg1) { return nwg1 * kSplitCounterStride; }
 
 bool split_fits(const PrefillArgs& a, int64_t nwg1) {
