@@ -73,9 +73,9 @@ int wrs_attn_synchronize(wrs_attn_ctx *ctx);
  * reference's tiling is fixed (Q_TILE = KV_TILE = 128, attention.rs:13,26).
  * prefill_queries: queries per workgroup of the f16/bf16 kernel: 256 or 128
  * (four waves), -256, -192 or -128 for that many queries on eight, twelve or
- * eight waves whose halves take alternate 64-key tiles (key halves), -64 for
- * 128-query blocks on two such workgroups each (merged through context
- * scratch, allocated at the first such call), 32 for the key split (four
+ * eight waves whose halves take alternate 64-key tiles (key halves), -2 or -3
+ * for 128-query blocks on that many such workgroups each (merged through
+ * context scratch, allocated at the first such call), 32 for the key split (four
  * waves share a 32-query block's keys), or 0 to choose by grid size (the
  * default). f32_split: -1 chooses by
  * grid size (the default), 0 runs 128-query blocks, 1 the four-wave key

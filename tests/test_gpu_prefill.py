@@ -28,14 +28,14 @@ def ctx(wrs):
     return c
 
 
-@pytest.fixture(params=[32, -64, -128, -192, -256, 128, 256],
-                ids=["ks32", "ws2", "kh128", "kh192", "kh256", "wg128", "wg256"])
+@pytest.fixture(params=[32, -2, -3, -128, -192, -256, 128, 256],
+                ids=["ks32", "ws2", "ws3", "kh128", "kh192", "kh256", "wg128", "wg256"])
 def schedule(request, ctx):
     """Every schedule of the 16-bit kernel on the same shapes: 4-wave
     workgroups of 256 or 128 queries, blocks of 256, 192 or 128 queries on
     8 or 12 waves whose halves take alternate 64-key tiles (key halves,
     -256 / -192 / -128), 128-query blocks split over two such workgroups
-    and merged through memory (-64), and the key split (32 queries, four
+    and merged through memory (-2 / -3 workgroups per block), and the key split (32 queries, four
     waves over the keys). By default the grid size picks one."""
     ctx.set_schedule(prefill_queries=request.param)
     yield request.param

@@ -82,7 +82,7 @@ constexpr int kDmaPerTile = 2 * kRowGroups;   // K and V
 // each).
 constexpr int kSplitPartWave = 18 * 64;
 constexpr int kSplitCounterStride = 32;
-constexpr int kSplitWays = 2;  // workgroups per split block
+constexpr int kSplitPartWg = 2 * kWaves * kSplitPartWave;  // one split workgroup's partial
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSumLimit = 16384.0f;  // row sum of one step that forces a rescale
 constexpr float kNoMax = -1.0e30f;     // reference max before the first step
@@ -256,8 +256,8 @@ template <typename T, int QB, int KH, int QW = kWaves, int WS = 1>
 __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     PrefillArgs a, int n_qblk) {
   static_assert(KH == 1 || KH == 2, "one or two key halves");
-  static_assert(WS == 1 || (WS == 2 && KH == 2 && QB == 1 && QW == kWaves),
-                "blocks split over two workgroups: 128 queries, key halves");
+  static_assert(WS == 1 || ((WS == 2 || WS == 3) && KH == 2 && QB == 1 && QW == kWaves),
+                "blocks split over two or three workgroups: 128 queries, key halves");
   static_assert(QW == kWaves || (QW == 6 && QB == 1 && KH == 2),
                 "six query waves: one block each, key halves");
   constexpr int kQB = QB;
@@ -768,8 +768,7 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     // counter and writes the output; the others are done. The fold takes the
     // partials in split order whichever workgroup runs it, so the bits do not
     // depend on which one finishes last.
-    static_assert(WS == 2 && kQB == 1, "the fold below takes two partials of one block");
-    constexpr int kPart = KH * kWaves * kSplitPartWave;
+    constexpr int kPart = kSplitPartWg;
     const int pw = (half * kWaves + wq) * kSplitPartWave + lane;
     {
       float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + wsplit) * kPart + pw;
@@ -793,30 +792,45 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     __syncthreads();
     if (!merger) return;
     {
-      const float* const p =
-          a.split_part + (static_cast<int64_t>(blk) * WS + (1 - wsplit)) * kPart + pw;
-      float ox[16];
+      // The other workgroups' partials; split s's is (m_s, l_s, O_s).
+      float px[WS][16], pm[WS], pl[WS];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) ox[i] = ld_agent(p + i * 64);
-      const float mx = ld_agent(p + 16 * 64), lx = ld_agent(p + 17 * 64);
-      // Split 0's partial is (m0, l0, O0) and split 1's (m1, l1, O1).
-      const bool own0 = wsplit == 0;
-      const float m0 = own0 ? m[0] : mx, m1 = own0 ? mx : m[0];
-      const float l0 = own0 ? l[0] : lx, l1 = own0 ? lx : l[0];
-      const float mm = fmaxf(m0, m1);
-      const float e0 = __builtin_amdgcn_exp2f(m0 - mm), e1 = __builtin_amdgcn_exp2f(m1 - mm);
-      l[0] = l0 * e0 + l1 * e1;
+      for (int s2 = 0; s2 < WS; ++s2) {
+        pm[s2] = pl[s2] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) px[s2][i] = 0.f;
+        if (s2 == wsplit) continue;
+        const float* const p = a.split_part + (static_cast<int64_t>(blk) * WS + s2) * kPart + pw;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) px[s2][i] = ld_agent(p + i * 64);
+        pm[s2] = ld_agent(p + 16 * 64);
+        pl[s2] = ld_agent(p + 17 * 64);
+      }
+      float ms[WS], e[WS];
+#pragma unroll
+      for (int s2 = 0; s2 < WS; ++s2) ms[s2] = s2 == wsplit ? m[0] : pm[s2];
+      float mm = ms[0];
+#pragma unroll
+      for (int s2 = 1; s2 < WS; ++s2) mm = fmaxf(mm, ms[s2]);
+#pragma unroll
+      for (int s2 = 0; s2 < WS; ++s2) e[s2] = __builtin_amdgcn_exp2f(ms[s2] - mm);
+      float lsum = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < WS; ++s2) lsum += (s2 == wsplit ? l[0] : pl[s2]) * e[s2];
       auto fold = [&](f32x16& ob) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float o0 = own0 ? ob[i] : ox[i], o1 = own0 ? ox[i] : ob[i];
-          ob[i] = o0 * e0 + o1 * e1;
+          float v = 0.f;
+#pragma unroll
+          for (int s2 = 0; s2 < WS; ++s2) v += (s2 == wsplit ? ob[i] : px[s2][i]) * e[s2];
+          ob[i] = v;
         }
       };
       if (half == 0)
         fold(o[0][0]);
       else
         fold(o[0][1]);
+      l[0] = lsum;
       m[0] = mm;
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1338,25 +1352,33 @@ bool prefill_mfma16_supports(const PrefillArgs& a) {
 
 namespace {
 
-// Scratch of a grid of nwg1 split 128-query blocks.
-int64_t split_floats(int64_t nwg1) { return nwg1 * kSplitWays * 2 * kWaves * kSplitPartWave; }
+// Workgroups per split block: as forced (-2 or -3), else three where that
+// still fits one round of workgroups, else two.
+int split_ways(const PrefillArgs& a, int64_t nwg1, int64_t cus) {
+  if (a.force_queries == -2 || a.force_queries == -3) return -a.force_queries;
+  return 3 * nwg1 <= cus ? 3 : 2;
+}
+
+// Scratch of a grid of nwg1 128-query blocks split `ways` ways.
+int64_t split_floats(int64_t nwg1, int ways) { return nwg1 * ways * kSplitPartWg; }
 int64_t split_words(int64_t nwg1) { return nwg1 * kSplitCounterStride; }
 
-bool split_fits(const PrefillArgs& a, int64_t nwg1) {
+bool split_fits(const PrefillArgs& a, int64_t nwg1, int ways) {
   return a.split_part && a.split_counters &&
-         split_floats(nwg1) <= static_cast<int64_t>(a.split_part_floats) &&
+         split_floats(nwg1, ways) <= static_cast<int64_t>(a.split_part_floats) &&
          split_words(nwg1) <= static_cast<int64_t>(a.split_counter_words);
 }
 
-// Does the schedule split each 128-query block over two workgroups? By
+// Does the schedule split each 128-query block over several workgroups? By
 // default for grids of fewer 128-query blocks than half the CUs (which then
-// run two workgroups of 8 waves per block) over at least 1024 keys: one
-// whisper-tiny or -base window, 72 or 96 blocks, 14.9 against 18.2 us with
-// the key split. Over fewer keys the merge through memory costs more than it
-// saves (448 keys, 24 blocks: 9.8 against 7.2 us).
+// run two or three workgroups of 8 waves per block) over at least 1152 keys:
+// one whisper-tiny window, 72 blocks, 12.5 against 18.2 us with the key split
+// (three ways); one whisper-base window, 96 blocks, 14.4 against 18.2 us (two
+// ways). Over fewer keys the merge through memory costs more than it saves
+// (a whisper-tiny shape over 1024 frames: 10.9 against 9.2 us).
 bool split_schedule(const PrefillArgs& a, int64_t nwg1, int64_t cus) {
-  return a.force_queries == -64 ||
-         (a.force_queries == 0 && 2 * nwg1 < cus && a.t_kv >= 1024);
+  return a.force_queries == -2 || a.force_queries == -3 ||
+         (a.force_queries == 0 && 2 * nwg1 < cus && a.t_kv >= 1152);
 }
 
 int64_t blocks128(const PrefillArgs& a) {
@@ -1368,12 +1390,14 @@ int64_t blocks128(const PrefillArgs& a) {
 
 void prefill_mfma16_scratch(const PrefillArgs& a, size_t* part_floats, size_t* counter_words) {
   const int64_t nwg1 = blocks128(a);
-  const bool used = a.t_q > 0 && nwg1 > 0 && split_schedule(a, nwg1, device_cus());
-  *part_floats = used ? static_cast<size_t>(split_floats(nwg1)) : 0;
+  const int64_t cus = device_cus();
+  const bool used = a.t_q > 0 && nwg1 > 0 && split_schedule(a, nwg1, cus);
+  *part_floats = used ? static_cast<size_t>(split_floats(nwg1, split_ways(a, nwg1, cus))) : 0;
   *counter_words = used ? static_cast<size_t>(split_words(nwg1)) : 0;
 }
 
-size_t prefill_split_floats_min() { return static_cast<size_t>(split_floats(device_cus() / 2)); }
+// The default schedule splits grids of at most one workgroup per CU.
+size_t prefill_split_floats_min() { return static_cast<size_t>(device_cus()) * kSplitPartWg; }
 size_t prefill_split_words_min() { return static_cast<size_t>(split_words(device_cus() / 2)); }
 
 hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) {
@@ -1395,8 +1419,9 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   // - half the CUs <= n <= 1 per CU: 128-query blocks on 8-wave workgroups
   //   with key halves (one large-v3 window, 240 blocks: 21.5 against 25.7 us;
   //   one whisper-small window, 144 blocks: 18.6 against 21.4);
-  // - fewer, over at least 1024 keys: each block on two such workgroups,
-  //   each over half its keys, merged through memory (split_schedule);
+  // - fewer, over at least 1152 keys: each block on two or three such
+  //   workgroups, each over its share of the keys, merged through memory
+  //   (split_schedule);
   // - fewer otherwise: the key split (32-query workgroups), which spreads a
   //   block over four CUs. It streams a block's K/V per 32 queries, 4x the
   //   bytes per FLOP of the 128-query kernel, which caps it near 50 GB/s per
@@ -1405,7 +1430,8 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   // in which each workgroup's fixed costs (q and the first tiles, the output
   // rows) are not hidden. a.force_queries forces one schedule: 256 or 128
   // queries per 4-wave workgroup, -256, -192 or -128 that many on 8 or 12
-  // waves with key halves, -64 the split blocks, 32 the key split.
+  // waves with key halves, -2 or -3 the split blocks over that many
+  // workgroups, 32 the key split.
   constexpr int kM1 = queries_per_wg<1>();
   constexpr int kM6 = queries_per_wg<1, 6>();
   const int64_t nwg1 = ((a.t_q + kM1 - 1) / kM1) * bh;
@@ -1420,10 +1446,12 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s) 
   if (a.force_queries == 128 || (by_grid && nwg1 > cus)) return launch_qb<1, 1>(a, dt, s);
   if (a.force_queries == -128 || (by_grid && 2 * nwg1 >= cus)) return launch_qb<1, 2>(a, dt, s);
   if (split_schedule(a, nwg1, cus)) {
-    if (split_fits(a, nwg1)) return launch_qb<1, 2, kWaves, kSplitWays>(a, dt, s);
+    const int ways = split_ways(a, nwg1, cus);
+    if (split_fits(a, nwg1, ways))
+      return ways == 3 ? launch_qb<1, 2, kWaves, 3>(a, dt, s) : launch_qb<1, 2, kWaves, 2>(a, dt, s);
     // No scratch (a call under stream capture before any outside it): the
     // key split below, unless forced.
-    if (a.force_queries == -64) return hipErrorInvalidValue;
+    if (!by_grid) return hipErrorInvalidValue;
   }
   const int n_qblk = (a.t_q + kKsQ - 1) / kKsQ;
   const int64_t nwg = n_qblk * bh;

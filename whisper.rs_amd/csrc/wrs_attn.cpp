@@ -534,10 +534,11 @@ int wrs_attn_set_schedule(wrs_attn_ctx* c, int prefill_queries, int f32_split) {
   if (!c) return WRS_EINVAL;
   std::lock_guard<std::mutex> lk(c->mu);
   if (prefill_queries != 0 && prefill_queries != 32 && prefill_queries != 128 &&
-      prefill_queries != 256 && prefill_queries != -64 && prefill_queries != -128 &&
+      prefill_queries != 256 && prefill_queries != -2 && prefill_queries != -3 &&
+      prefill_queries != -128 &&
       prefill_queries != -192 && prefill_queries != -256)
     return fail(c, WRS_EINVAL,
-                "prefill_queries must be 0, 32, 128, 256, -64, -128, -192 or -256");
+                "prefill_queries must be 0, 32, 128, 256, -2, -3, -128, -192 or -256");
   if (f32_split < -1 || f32_split > 4)
     return fail(c, WRS_EINVAL, "f32_split must be -1..4");
   c->prefill_queries = prefill_queries;
