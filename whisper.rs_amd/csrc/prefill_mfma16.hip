@@ -251,7 +251,9 @@ static_assert(pipe_order_ok<1>() && pipe_order_ok<2>(), "pipelined step order");
 // same layout). For grids of at most one such workgroup per CU, it puts two
 // waves (three with QW = 6) on every SIMD of the CUs in use instead of one.
 // With QW = 6 the first four waves of a half move its tiles and the other
-// two only compute.
+// two only compute. WS > 1 (split blocks): a block's keys are shared by WS
+// such workgroups, its tiles falling into KH * WS parts taken in turn, and
+// the workgroups merge through memory.
 template <typename T, int QB, int KH, int QW = kWaves, int WS = 1>
 __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
     PrefillArgs a, int n_qblk) {
@@ -283,8 +285,8 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hl = lane >> 5;
-  // Key half of this wave, its place among the half's four waves, and the
-  // half's tile ring.
+  // Key half of this wave, its place among the half's waves, and the half's
+  // tile ring.
   const int half = KH == 1 ? 0 : QW == kWaves ? (wave >> 2) : wave / QW;
   const int wq = KH == 1 ? wave : QW == kWaves ? (wave & 3) : wave - QW * half;
   // The first four waves of a half move its tiles (16 rows of each apiece).
