@@ -28,15 +28,16 @@ def ctx(wrs):
     return c
 
 
-@pytest.fixture(params=[32, -2, -3, -128, -192, -256, 128, 256],
-                ids=["ks32", "ws2", "ws3", "kh128", "kh192", "kh256", "wg128", "wg256"])
+@pytest.fixture(params=[0, 32, -2, -3, -128, -192, -256, 128, 256],
+                ids=["default", "ks32", "ws2", "ws3", "kh128", "kh192", "kh256", "wg128", "wg256"])
 def schedule(request, ctx):
     """Every schedule of the 16-bit kernel on the same shapes: 4-wave
     workgroups of 256 or 128 queries, blocks of 256, 192 or 128 queries on
     8 or 12 waves whose halves take alternate 64-key tiles (key halves,
-    -256 / -192 / -128), 128-query blocks split over two such workgroups
-    and merged through memory (-2 / -3 workgroups per block), and the key split (32 queries, four
-    waves over the keys). By default the grid size picks one."""
+    -256 / -192 / -128), 128-query blocks split over two or three such
+    workgroups and merged through memory (-2 / -3), and the key split (32
+    queries, four waves over the keys); and the default, by which the grid
+    size picks one."""
     ctx.set_schedule(prefill_queries=request.param)
     yield request.param
     ctx.set_schedule()
@@ -204,9 +205,15 @@ def test_large_encoder_bf16(wrs, orc, ctx, schedule):
     vmax = v.max(axis=1)
     assert np.all(out >= vmin[:, None, :] - 1e-3) and np.all(out <= vmax[:, None, :] + 1e-3)
     # a window computed alone equals the same window inside the batch, bitwise
+    # under one schedule; by default the grid size picks the schedule, and the
+    # two grids round the weights against different running maxima, each
+    # within TOL16 of the oracle
     note("device prefill bf16: window 7 alone")
     alone = _encoder_run(wrs, ctx, cfg, q[7:8], k[7:8], v[7:8], torch.bfloat16, batch=1)
-    assert np.array_equal(alone[0], out[7])
+    if schedule == 0:
+        assert maxerr(alone[0], out[7]) <= 2 * TOL16
+    else:
+        assert np.array_equal(alone[0], out[7])
 
 
 @pytest.mark.parametrize("t", [1000, 1500])
@@ -234,7 +241,10 @@ def test_prefill_many_query_blocks(wrs, ctx, t, schedule):
     for b in range(B):
         wrs.prefill(qd[b:b + 1], kd[b:b + 1], vd[b:b + 1], one, batch=1, n_heads=H, t_q=t,
                     t_kv=t, d_head=64, q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
-        assert np.array_equal(got[b], host(one)[0]), f"window {b}"
+        if schedule == 0:  # the two grids may take different schedules
+            assert maxerr(got[b], host(one)[0]) <= 2 * TOL16, f"window {b}"
+        else:
+            assert np.array_equal(got[b], host(one)[0]), f"window {b}"
     for b in (0, 17, B - 1):
         ref = attention_f64(q[b], k[b], v[b], t, t, H, dm)
         assert maxerr(got[b], ref) <= TOL16, f"window {b}"
