@@ -550,3 +550,41 @@ def test_bf16_v_beyond_f16_range_everywhere(wrs, orc, ctx):
         rel = _colscaled_err(out[w], ref, v[w])
         note(f"  window {w}: max|gpu - oracle| over max|V column| = {rel:.3e}")
         assert rel <= TOL32
+
+
+@pytest.mark.parametrize("ways", [2, 3])
+def test_split_blocks_repeated_launches(wrs, ctx, ways):
+    # Split blocks merge through a counter per block that the merging workgroup
+    # re-arms: 200 launches in a row, alternating two inputs, each give the
+    # bits of the first launch with the same input (a counter left off zero
+    # would make a block merge early or never).
+    from wrs_amd import workloads as W
+    H, T = 6, 1500
+    dm = H * 64
+    note(f"split blocks over {ways} workgroups: 200 launches, two alternating inputs")
+    xs = [[dev(W.normal((T, dm), 90 + 3 * i + j, storage="f16"), torch.float16)
+           for j in range(3)] for i in range(2)]
+    lay = wrs.token_major(T, dm, 64)
+    ctx.set_schedule(prefill_queries=-ways)
+    try:
+        outs = [torch.empty((T, dm), dtype=torch.float32, device="cuda") for _ in range(2)]
+        for i in range(2):
+            wrs.prefill(*xs[i], outs[i], batch=1, n_heads=H, t_q=T, t_kv=T, d_head=64,
+                        q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+        ref = [host(o).copy() for o in outs]
+        for i in range(2):
+            assert maxerr(ref[i], attention_f64(*(host(x) for x in xs[i]), T, T, H, dm)) <= TOL16
+        bad = 0
+        for n in range(200):
+            i = n % 2
+            outs[i].fill_(float("nan"))
+            wrs.prefill(*xs[i], outs[i], batch=1, n_heads=H, t_q=T, t_kv=T, d_head=64,
+                        q_layout=lay, kv_layout=lay, out_layout=lay, ctx=ctx)
+            if n % 20 == 19 or n == 0:
+                bad += int(not np.array_equal(host(outs[i]), ref[i]))
+        torch.cuda.synchronize()
+        assert bad == 0
+        for i in range(2):
+            assert np.array_equal(host(outs[i]), ref[i])
+    finally:
+        ctx.set_schedule()
