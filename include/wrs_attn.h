@@ -156,7 +156,10 @@ int wrs_mha_with_cache(wrs_attn_ctx *ctx, const float *q, size_t q_len, const fl
  * of 8 elements). The 16-bit kernel forms the PV product in f16: for bf16
  * inputs, a workgroup whose outputs come out inf/NaN (a V value of magnitude
  * >= 65536) recomputes its queries with f32 operands in the same launch, so
- * any finite bf16 input gives a finite, f32-accurate result. */
+ * any finite bf16 input gives a finite, f32-accurate result. Grids of fewer
+ * 128-query blocks than half the CUs over long key ranges (one whisper-tiny
+ * or -base window) merge split blocks through a context buffer that the first
+ * such call outside stream capture allocates (wrs_attn_reserve). */
 int wrs_attn_prefill(wrs_attn_ctx *ctx, int q_dtype, const void *q, const wrs_layout *q_layout,
                      int kv_dtype, const void *k, const wrs_layout *k_layout, const void *v,
                      const wrs_layout *v_layout, float *out, const wrs_layout *out_layout,
