@@ -588,3 +588,39 @@ def test_split_blocks_repeated_launches(wrs, ctx, ways):
             assert np.array_equal(host(outs[i]), ref[i])
     finally:
         ctx.set_schedule()
+
+
+def _random_shapes(n=10, seed=0x5EED_0F):
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for _ in range(n):
+        causal = bool(rng.integers(2))
+        shapes.append((int(rng.integers(1, 4)), int(rng.integers(1, 6)), int(rng.integers(1, 700)),
+                       int(rng.integers(1, 1300)), causal,
+                       int(rng.integers(0, 300)) if causal else 0,
+                       "bf16" if rng.integers(2) else "f16"))
+    return shapes
+
+
+@pytest.mark.parametrize("B,H,t_q,t_kv,causal,offset,dtype", _random_shapes())
+def test_prefill_random_shapes(wrs, ctx, B, H, t_q, t_kv, causal, offset, dtype, schedule):
+    # Seeded random batch, head, length, mask and type combinations under every
+    # schedule, against the float64 reference: ragged tile counts per key part,
+    # partial query blocks and masked tails in one launch.
+    from wrs_amd import workloads as W
+    dm = H * 64
+    note(f"device prefill {dtype} B={B} H={H} t_q={t_q} t_kv={t_kv} causal={causal} "
+         f"offset={offset}")
+    q = W.normal((B, t_q, dm), 51, storage=dtype)
+    k = W.normal((B, t_kv, dm), 52, storage=dtype)
+    v = W.normal((B, t_kv, dm), 53, storage=dtype)
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    out = torch.full((B, t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, 64), wrs.token_major(t_kv, dm, 64)
+    wrs.prefill(dev(q, tdt), dev(k, tdt), dev(v, tdt), out, batch=B, n_heads=H, t_q=t_q,
+                t_kv=t_kv, d_head=64, q_layout=lq, kv_layout=lk, out_layout=lq,
+                causal=causal, q_pos_offset=offset, ctx=ctx)
+    got = host(out)
+    for b in range(B):
+        ref = attention_f64(q[b], k[b], v[b], t_q, t_kv, H, dm, causal=causal, q_offset=offset)
+        assert maxerr(got[b], ref) <= TOL16, b
