@@ -18,11 +18,6 @@ using f32blk::kThreads;
 using f32blk::Tiles;
 using f32blk::f32x16;
 
-__device__ inline int xcd_remap(int pid, int nwg) {
-  const int xcd = pid & 7, k = pid >> 3;
-  const int per = nwg >> 3, rem = nwg & 7;
-  return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
-}
 
 template <typename QT, typename KT, int DB>
 __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, int n_qblk) {

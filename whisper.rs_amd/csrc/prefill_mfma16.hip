@@ -177,16 +177,6 @@ __device__ inline uint32_t lds_addr(const void* p) {
       reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
 }
 
-// Logical workgroup id with an XCD-aware remap: the hardware hands linear ids
-// round-robin to the 8 XCDs, so consecutive logical ids (the query blocks of
-// one (window, head), which read the same K/V) are gathered onto one XCD and
-// share its L2.
-__device__ inline int xcd_remap(int pid, int nwg) {
-  const int xcd = pid & 7, k = pid >> 3;
-  const int per = nwg >> 3, rem = nwg & 7;
-  return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
-}
-
 // This wave's LDS traffic is complete, then all waves meet (no vmcnt wait:
 // tile loads in flight stay in flight).
 __device__ inline void tile_barrier() {

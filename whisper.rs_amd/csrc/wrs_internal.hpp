@@ -36,6 +36,16 @@ struct Layout {
 
 // Flash-attention prefill over full query/key sequences
 // (crates/tensor/src/ops/attention.rs:68-243 semantics).
+// Logical workgroup id with an XCD-aware remap: the hardware hands linear ids
+// round-robin to the 8 XCDs, so consecutive logical ids (the query blocks of
+// one (window, head), which read the same K/V) are gathered onto one XCD and
+// share its L2.
+__device__ inline int xcd_remap(int pid, int nwg) {
+  const int xcd = pid & 7, k = pid >> 3;
+  const int per = nwg >> 3, rem = nwg & 7;
+  return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
+}
+
 // Agent-scope (L2-coherent across the GPU's XCDs) store and load of one
 // float, for partials that another workgroup of the launch merges.
 __device__ inline void st_agent(float* p, float v) {
