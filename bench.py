@@ -745,6 +745,29 @@ def bench_rows(wrs, ctx, reps):
     return res
 
 
+def device_call_ms(ctx, run, out, reps: int, per_graph: int = 10) -> float:
+    """Mean time of one launch of `run` (which writes `out`), in ms, from HIP
+    graph replays of `per_graph` launches checked against the eager result:
+    timed from the host, launches shorter than its call path would time the
+    host instead."""
+    import torch
+    run()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.use_torch_stream()
+        for _ in range(per_graph):
+            run()
+    ctx.use_torch_stream()
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(out, eager):
+        raise RuntimeError("graph replay of the launch differs from eager")
+    return _replay_time_us(g, max(1, reps), per_graph) / 1e3
+
+
 def host_call_ms(fn, reps: int) -> dict:
     """Per-call wall times of a synchronous host-slice call, in ms: the
     median (the figure reported; single calls through pageable host memory
@@ -779,13 +802,7 @@ def bench_host_slice(wrs, W, ctx, reps=20):
     for _ in range(20):
         run()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        run()
-    e1.record()
-    e1.synchronize()
-    dev_ms = e0.elapsed_time(e1) / reps
+    dev_ms = device_call_ms(ctx, run, od, reps)
     gflop = cfg.flops() / 1e9
     return {"workload": cfg.name, "unit": "GFLOP/s",
             "host_slice_ms": round(host_ms, 3), "host_slice_value": round(gflop / host_ms * 1e3, 1),
@@ -837,13 +854,7 @@ def bench_reference_shapes(wrs, ctx, reps=20):
         for _ in range(20):
             run()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            run()
-        e1.record()
-        e1.synchronize()
-        dev_ms = e0.elapsed_time(e1) / reps
+        dev_ms = device_call_ms(ctx, run, od, reps)
         gflop = 4.0 * H * t_q * t_kv * 64 / 1e9
         res[f"{t_q}x{t_kv}"] = {
             "host_slice_ms": round(host_ms, 4),

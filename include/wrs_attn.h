@@ -79,7 +79,9 @@ int wrs_attn_synchronize(wrs_attn_ctx *ctx);
  * waves share a 32-query block's keys), or 0 to choose by grid size (the
  * default). f32_split: -1 chooses by
  * grid size (the default), 0 runs 128-query blocks, 1 the four-wave key
- * split, 2..4 the key split over that many waves. Other values: WRS_EINVAL. */
+ * split, 2..4 the key split over that many waves, 5 the four-wave key split
+ * with each block over several workgroups (merged through the same context
+ * buffer). Other values: WRS_EINVAL. */
 int wrs_attn_set_schedule(wrs_attn_ctx *ctx, int prefill_queries, int f32_split);
 /* Text of the last error on this context (valid until the next call). */
 const char *wrs_attn_last_error(wrs_attn_ctx *ctx);

@@ -87,10 +87,10 @@ class Context:
         (``wrs_attn_set_schedule``): queries per workgroup of the f16/bf16
         kernel (256 or 128; -256, -192 or -128 for key halves on 8 or 12
         waves; -2 or -3 for 128-query blocks split over that many such
-        workgroups; 32
-        for the key split; 0 = by grid size) and the
-        f32 kernel's key split
-        (-1 = by grid size, 0 = 128-query blocks, 1..4 = key split)."""
+        workgroups; 32 for the key split; 0 = by grid size) and the f32
+        kernel's key split (-1 = by grid size, 0 = 128-query blocks, 1..4 =
+        key split over four or that many waves, 5 = the four-wave key split
+        with each block over several workgroups)."""
         self.check(self._lib.wrs_attn_set_schedule(self.handle, int(prefill_queries),
                                                    int(f32_split)), "wrs_attn_set_schedule")
 

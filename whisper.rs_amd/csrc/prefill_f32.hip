@@ -34,13 +34,21 @@ __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, in
 // in turn (tile t on wave t % S). Each wave keeps its own online softmax over
 // its tiles, in its own LDS tile pair, with the next tile's rows loading while
 // it computes. The workgroup then merges the S (max, sum, O) by the
-// log-sum-exp rule.
+// log-sum-exp rule. Grids of fewer such blocks than half the CUs (a 64-query
+// cross-attention call: 12 blocks for 6 heads) spread each block over `ws`
+// workgroups, wave w of workgroup s taking the block's tiles s S + w,
+// s S + w + S ws, ...; each workgroup publishes its merged (max, sum, O) rows
+// with agent-scope stores, and the last of the block's workgroups to count in
+// folds them in split order (bits independent of arrival order), re-arms the
+// block's counter and writes the rows.
 constexpr int kQS = 32;       // queries per k-split workgroup
 constexpr int kMaxSplit = 4;  // waves per k-split workgroup, at most
+constexpr int kMaxWs = 16;    // workgroups per block, at most
+constexpr int kWsCounterStride = 32;  // words between merge counters (one 128-byte line)
 
 template <typename QT, typename KT, int DB>
 __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f32_ksplit(
-    PrefillArgs a, int n_qblk, int vec) {
+    PrefillArgs a, int n_qblk, int vec, int ws) {
   constexpr int D = 32 * DB;
   constexpr int P = Tiles<DB>::P;
   constexpr int kN = f32blk::kN;
@@ -50,13 +58,17 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
   typedef float f32x4 __attribute__((ext_vector_type(4)));
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int qblk = lid % n_qblk;
-  const int bh = lid / n_qblk;
+  // A block's ws workgroups are neighbours in lid (one XCD).
+  const int wsplit = lid % ws, blk = lid / ws;
+  const int qblk = blk % n_qblk;
+  const int bh = blk / n_qblk;
   const int h = bh % a.n_heads, b = bh / a.n_heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int S = __builtin_amdgcn_readfirstlane(static_cast<int>(blockDim.x) >> 6);
+  // This wave's first tile and the stride between its tiles.
+  const int j_first = (wsplit * S + wave) * kN, j_step = S * ws * kN;
   const int r32 = lane & 31, hl = lane >> 5;
   const int dh = a.d_head;
   float* const Ks = tl[wave].k;
@@ -152,9 +164,9 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
           vr[i] = ok ? *reinterpret_cast<const f32x4*>(vrow + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
       };
-      int j0 = wave * kN;
+      int j0 = j_first;
       if (j0 < kv_end) load(j0);
-      for (; j0 < kv_end; j0 += S * kN) {
+      for (; j0 < kv_end; j0 += j_step) {
         wave_sync();
 #pragma unroll
         for (int i = 0; i < D / 8; ++i)
@@ -164,13 +176,13 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
             Vs[key * P + c0 + 4 * i + c] = vr[i][c];
           }
         wave_sync();
-        if (j0 + S * kN < kv_end) load(j0 + S * kN);
+        if (j0 + j_step < kv_end) load(j0 + j_step);
         tile(j0);
       }
     }
   }
   if (!(std::is_same<KT, float>::value && vec)) {
-    for (int j0 = wave * kN; j0 < kv_end; j0 += S * kN) {
+    for (int j0 = j_first; j0 < kv_end; j0 += j_step) {
       wave_sync();
 #pragma unroll 4
       for (int e = lane; e < kN * D; e += 64) {
@@ -206,6 +218,10 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
   }
   __syncthreads();
   // Thread t merges element e = t, t + 64S, ... of the block's 32 x dh outputs.
+  // With ws > 1 it publishes (max, sum, unnormalized O) instead: rows of
+  // dh + 2 floats, [max, sum, O...], per (block, split).
+  const int pitch = dh + 2;
+  float* const mine = a.split_part + (static_cast<int64_t>(blk) * ws + wsplit) * kQS * pitch;
   for (int e = tid; e < kQS * dh; e += 64 * S) {
     const int mq = e / dh, d = e % dh;
     const int oq = qblk * kQS + mq;
@@ -220,9 +236,72 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
       L += ew * t[kQS * R + kQS + mq];
       acc += ew * t[mq * R + d];
     }
-    a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] =
-        acc * ((L > 0.f) ? 1.f / L : 0.f);
+    if (ws == 1) {
+      a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] =
+          acc * ((L > 0.f) ? 1.f / L : 0.f);
+    } else {
+      st_agent(mine + mq * pitch + 2 + d, acc);
+      if (d == 0) {
+        st_agent(mine + mq * pitch, M);
+        st_agent(mine + mq * pitch + 1, L);
+      }
+    }
   }
+  if (ws == 1) return;
+  __shared__ int merger;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  unsigned* const counter = a.split_counters + static_cast<int64_t>(blk) * kWsCounterStride;
+  if (tid == 0)
+    merger = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             static_cast<unsigned>(ws - 1);
+  __syncthreads();
+  if (!merger) return;
+  // The fold: the rows' max and sum of every split into LDS (the tile
+  // buffers are free), then per row the weight of each split and the total
+  // sum, then each output element from its splits' partial sums, all of an
+  // element's loads in flight at once.
+  const float* const all = a.split_part + static_cast<int64_t>(blk) * ws * kQS * pitch;
+  float* const sm = reinterpret_cast<float*>(&tl[0]);  // [kMaxWs][kQS] max, then weight
+  float* const sl = sm + kMaxWs * kQS;                 // [kMaxWs][kQS] sum
+  float* const sinv = sl + kMaxWs * kQS;               // [kQS] 1 / total sum, or 0
+  static_assert(sizeof(Tiles<DB>) >= (2 * kMaxWs + 1) * kQS * sizeof(float), "fold fits");
+  for (int i = tid; i < ws * kQS; i += 64 * S) {
+    const float* const r = all + i * pitch;  // split i / kQS, row i % kQS
+    const float mx = ld_agent(r), lx = ld_agent(r + 1);
+    sm[i] = mx;
+    sl[i] = lx;
+  }
+  __syncthreads();
+  if (tid < kQS) {
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < ws; ++s2) M = fmaxf(M, sm[s2 * kQS + tid]);
+    float L = 0.f;
+    for (int s2 = 0; s2 < ws; ++s2) {
+      const float ms = sm[s2 * kQS + tid];
+      const float es = (ms == -INFINITY) ? 0.f : expf(ms - M);
+      sm[s2 * kQS + tid] = es;
+      L += es * sl[s2 * kQS + tid];
+    }
+    sinv[tid] = (L > 0.f) ? 1.f / L : 0.f;
+  }
+  __syncthreads();
+  for (int e = tid; e < kQS * dh; e += 64 * S) {
+    const int mq = e / dh, d = e % dh;
+    const int oq = qblk * kQS + mq;
+    if (oq >= a.t_q) continue;
+    // Every slot loads (split 0's row past ws, weighted 0), so no branch
+    // stands between the loads.
+    float part[kMaxWs];
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxWs; ++s2)
+      part[s2] = ld_agent(all + ((s2 < ws ? s2 : 0) * kQS + mq) * pitch + 2 + d);
+    float acc = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxWs; ++s2) acc += (s2 < ws ? sm[s2 * kQS + mq] : 0.f) * part[s2];
+    a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] = acc * sinv[mq];
+  }
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // CUs of the current device, read once.
@@ -236,6 +315,29 @@ int device_cus() {
   return cus;
 }
 
+// Workgroups per 32-query block of the key split: by default as many as fill
+// the CUs (at most kMaxWs, at most one per eight of the block's 32-key tiles,
+// so each wave keeps two tiles or more) where the blocks occupy fewer than
+// half the CUs; forced (a.force_f32_split == 5) at least two. 1: no split.
+int ksplit_ways(const PrefillArgs& a, int64_t nws, int64_t cus) {
+  const int forced = a.force_f32_split;
+  if (forced != 5 && (forced != -1 || 2 * nws >= cus)) return 1;
+  const int64_t tiles = (a.t_kv + f32blk::kN - 1) / f32blk::kN;
+  int64_t ws = std::min<int64_t>({kMaxWs, cus / std::max<int64_t>(nws, 1),
+                                  std::max<int64_t>(1, tiles / kMaxSplit)});
+  if (forced == 5) ws = std::max<int64_t>(ws, 2);
+  return static_cast<int>(ws);
+}
+
+int64_t ksplit_floats(const PrefillArgs& a, int64_t nws, int ws) {
+  return nws * ws * kQS * (a.d_head + 2);
+}
+int64_t ksplit_words(int64_t nws) { return nws * kWsCounterStride; }
+
+int64_t blocks32(const PrefillArgs& a) {
+  return ((a.t_q + kQS - 1) / kQS) * static_cast<int64_t>(a.n_heads) * a.batch;
+}
+
 template <typename QT, typename KT>
 hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   const int n_qblk = (a.t_q + kM - 1) / kM;
@@ -245,7 +347,7 @@ hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   const int db = (a.d_head + 31) / 32;
   if (db < 1 || db > 4) return hipErrorInvalidValue;
   // a.force_f32_split: 0 forces 128-query blocks, 1 the key split, 2..4 the
-  // key split over that many waves.
+  // key split over that many waves, 5 the key split over several workgroups.
   const int forced = a.force_f32_split;
   // The key split, four waves per 32-query block, up to 4 blocks of 128
   // queries per CU; beyond that the 128-query blocks, whose four waves share
@@ -254,19 +356,27 @@ hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   // 1500 x 32 heads 279 against 347 us, 1500 x 320 heads 2447 against 2150 us.
   const int n_qs = (a.t_q + kQS - 1) / kQS;
   const int64_t nws = n_qs * bh;
-  const int split = forced >= 2 ? std::min(forced, kMaxSplit) : kMaxSplit;
+  const int split = forced >= 2 && forced <= 4 ? forced : kMaxSplit;
   if (forced >= 1 || (forced != 0 && nwg <= 4 * static_cast<int64_t>(device_cus()))) {
-    if (nws > 0x7fffffff) return hipErrorInvalidConfiguration;
+    int ws = ksplit_ways(a, nws, device_cus());
+    if (ws > 1 && !(a.split_part && a.split_counters &&
+                    ksplit_floats(a, nws, ws) <= static_cast<int64_t>(a.split_part_floats) &&
+                    ksplit_words(nws) <= static_cast<int64_t>(a.split_counter_words))) {
+      // No scratch (a call under stream capture before any outside it).
+      if (forced == 5) return hipErrorInvalidValue;
+      ws = 1;
+    }
+    if (nws * ws > 0x7fffffff) return hipErrorInvalidConfiguration;
     auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const int vec = a.d_head == 32 * db && a.lk.rs % 4 == 0 && a.lv.rs % 4 == 0 &&
                     a.lk.bs % 4 == 0 && a.lv.bs % 4 == 0 && a.lk.hs % 4 == 0 &&
                     a.lv.hs % 4 == 0 && al16(a.k) && al16(a.v);
-    const dim3 grid(static_cast<unsigned>(nws)), block(64 * split);
+    const dim3 grid(static_cast<unsigned>(nws * ws)), block(64 * split);
     switch (db) {
-      case 1: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 1>), grid, block, 0, s, a, n_qs, vec); break;
-      case 2: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 2>), grid, block, 0, s, a, n_qs, vec); break;
-      case 3: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 3>), grid, block, 0, s, a, n_qs, vec); break;
-      default: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 4>), grid, block, 0, s, a, n_qs, vec); break;
+      case 1: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 1>), grid, block, 0, s, a, n_qs, vec, ws); break;
+      case 2: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 2>), grid, block, 0, s, a, n_qs, vec, ws); break;
+      case 3: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 3>), grid, block, 0, s, a, n_qs, vec, ws); break;
+      default: hipLaunchKernelGGL((fa2_prefill_f32_ksplit<QT, KT, 4>), grid, block, 0, s, a, n_qs, vec, ws); break;
     }
     return hipGetLastError();
   }
@@ -282,6 +392,19 @@ hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+void prefill_f32_scratch(const PrefillArgs& a, size_t* part_floats, size_t* counter_words) {
+  *part_floats = *counter_words = 0;
+  const int64_t nws = blocks32(a);
+  if (a.t_q <= 0 || nws <= 0 || a.force_f32_split == 0) return;
+  const int64_t nwg = ((a.t_q + kM - 1) / kM) * static_cast<int64_t>(a.n_heads) * a.batch;
+  const int64_t cus = device_cus();
+  if (a.force_f32_split < 1 && nwg > 4 * cus) return;  // 128-query blocks
+  const int ws = ksplit_ways(a, nws, cus);
+  if (ws == 1) return;
+  *part_floats = static_cast<size_t>(ksplit_floats(a, nws, ws));
+  *counter_words = static_cast<size_t>(ksplit_words(nws));
+}
 
 hipError_t launch_prefill_f32(const PrefillArgs& a, DType q_dt, DType kv_dt, hipStream_t s) {
   if (q_dt == kF32 && kv_dt == kF32) return launch_typed<float, float>(a, s);

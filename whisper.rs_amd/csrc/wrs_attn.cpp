@@ -224,6 +224,28 @@ int run_exact(wrs_attn_ctx* c, const float* q, size_t q_floats, const float* k, 
   return WRS_OK;
 }
 
+// Scratch for a prefill schedule that splits blocks over workgroups (pf
+// floats of partials, cw counter words; 0 when it needs none). Outside capture
+// it is allocated here, at least the size every default split needs (so that
+// graphs captured later keep valid pointers), or grown for a forced schedule
+// on a larger grid; during capture the kernels take another schedule when
+// what exists does not fit. Hands the buffers to `a`.
+int split_scratch(wrs_attn_ctx* c, size_t pf, size_t cw, wrs::PrefillArgs& a) {
+  if (pf && !capturing(c)) {
+    int rc = grow(c, reinterpret_cast<void**>(&c->split_part), &c->split_part_bytes,
+                  std::max(pf, wrs::prefill_split_floats_min()) * sizeof(float), false);
+    if (rc) return rc;
+    rc = grow(c, reinterpret_cast<void**>(&c->split_counters), &c->split_counter_bytes,
+              std::max(cw, wrs::prefill_split_words_min()) * sizeof(unsigned), true);
+    if (rc) return rc;
+  }
+  a.split_part = c->split_part;
+  a.split_part_floats = c->split_part_bytes / sizeof(float);
+  a.split_counters = c->split_counters;
+  a.split_counter_words = c->split_counter_bytes / sizeof(unsigned);
+  return WRS_OK;
+}
+
 int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& lq, int kv_dtype,
                  const void* k, const wrs_layout& lk, const void* v, const wrs_layout& lv,
                  float* out, const wrs_layout& lo, size_t batch, size_t n_heads, size_t t_q,
@@ -274,28 +296,18 @@ int prefill_impl(wrs_attn_ctx* c, int q_dtype, const void* q, const wrs_layout& 
   };
   if (same16 && d_head == 64 && aligned16(q, lq, 8) && aligned16(k, lk, 8) &&
       aligned16(v, lv, 8) && aligned16(out, lo, 4) && wrs::prefill_mfma16_supports(a)) {
-    // Scratch for a schedule that splits blocks over workgroups. Outside
-    // capture it is allocated (or, for a forced schedule on a larger grid,
-    // grown) here; during capture the kernel takes another schedule when what
-    // exists does not fit.
     size_t pf = 0, cw = 0;
     wrs::prefill_mfma16_scratch(a, &pf, &cw);
-    if (pf && !capturing(c)) {
-      int rc = grow(c, reinterpret_cast<void**>(&c->split_part), &c->split_part_bytes,
-                    std::max(pf, wrs::prefill_split_floats_min()) * sizeof(float), false);
-      if (rc) return rc;
-      rc = grow(c, reinterpret_cast<void**>(&c->split_counters), &c->split_counter_bytes,
-                std::max(cw, wrs::prefill_split_words_min()) * sizeof(unsigned), true);
-      if (rc) return rc;
-    }
-    a.split_part = c->split_part;
-    a.split_part_floats = c->split_part_bytes / sizeof(float);
-    a.split_counters = c->split_counters;
-    a.split_counter_words = c->split_counter_bytes / sizeof(unsigned);
+    const int rc = split_scratch(c, pf, cw, a);
+    if (rc) return rc;
     WRS_HIP(c, wrs::launch_prefill_mfma16(a, q_dtype == WRS_F16 ? wrs::kF16 : wrs::kBF16,
                                           c->stream));
     return WRS_OK;
   }
+  size_t pf = 0, cw = 0;
+  wrs::prefill_f32_scratch(a, &pf, &cw);
+  const int rc = split_scratch(c, pf, cw, a);
+  if (rc) return rc;
   WRS_HIP(c, wrs::launch_prefill_f32(a, static_cast<DType>(q_dtype), static_cast<DType>(kv_dtype),
                                      c->stream));
   return WRS_OK;
@@ -539,8 +551,8 @@ int wrs_attn_set_schedule(wrs_attn_ctx* c, int prefill_queries, int f32_split) {
       prefill_queries != -192 && prefill_queries != -256)
     return fail(c, WRS_EINVAL,
                 "prefill_queries must be 0, 32, 128, 256, -2, -3, -128, -192 or -256");
-  if (f32_split < -1 || f32_split > 4)
-    return fail(c, WRS_EINVAL, "f32_split must be -1..4");
+  if (f32_split < -1 || f32_split > 5)
+    return fail(c, WRS_EINVAL, "f32_split must be -1..5");
   c->prefill_queries = prefill_queries;
   c->f32_split = f32_split;
   return WRS_OK;

@@ -34,8 +34,6 @@ struct Layout {
   int64_t rs;  // row (token) stride
 };
 
-// Flash-attention prefill over full query/key sequences
-// (crates/tensor/src/ops/attention.rs:68-243 semantics).
 // Logical workgroup id with an XCD-aware remap: the hardware hands linear ids
 // round-robin to the 8 XCDs, so consecutive logical ids (the query blocks of
 // one (window, head), which read the same K/V) are gathered onto one XCD and
@@ -55,6 +53,8 @@ __device__ inline float ld_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Flash-attention prefill over full query/key sequences
+// (crates/tensor/src/ops/attention.rs:68-243 semantics).
 struct PrefillArgs {
   const void* q;
   const void* k;
@@ -68,10 +68,10 @@ struct PrefillArgs {
   // Schedule overrides from the context (wrs_attn_set_schedule): queries per
   // workgroup of the 16-bit kernel (0 = by grid size), and the f32 kernel's
   // key split (-1 = by grid size, 0 = 128-query blocks, 1 = four waves,
-  // 2..4 = that many waves).
+  // 2..4 = that many waves, 5 = four waves over several workgroups).
   int force_queries;
   int force_f32_split;
-  // Context scratch for 16-bit grids whose blocks split their keys over two
+  // Context scratch for grids whose blocks split their keys over several
   // workgroups (null when none is available): partials and merge counters
   // (zero between launches), with their sizes.
   float* split_part;
@@ -94,6 +94,8 @@ hipError_t launch_prefill_mfma16(const PrefillArgs& a, DType dt, hipStream_t s);
 // f32-accumulate-check kernel on f32 MFMA: q f32, k/v f32|f16|bf16 widened
 // exactly to f32, any d_head <= 128.
 hipError_t launch_prefill_f32(const PrefillArgs& a, DType q_dt, DType kv_dt, hipStream_t s);
+// Scratch its schedule for `a` uses (as prefill_mfma16_scratch).
+void prefill_f32_scratch(const PrefillArgs& a, size_t* part_floats, size_t* counter_words);
 
 // Exact reference decode semantics on f32 K/V (attention.rs:246-434
 // single_token_mha_d64 and decoder.rs:835-892): full score row, softmax with
