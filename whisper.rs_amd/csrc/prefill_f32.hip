@@ -80,12 +80,34 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
 
   const int qi = qblk * kQS + r32;
   const int qpos = qi + a.q_pos_offset;
+  const int nth = 64 * S;
+  // The block's 32 query rows go through LDS (wave 0's K tile, pitch P) in
+  // coalesced loads shared by the S waves; each lane then takes its 32-row
+  // MFMA operand (d = 2 kk + hl) from there. Loads past the block's rows or
+  // d_head read row 0 of the head and are stored as 0.
   float qf[D / 2];
+  auto stage_q = [&] {
+    float* const qs = tl[0].k;
+    for (int e0 = 0; e0 < kQS * D; e0 += 8 * nth) {
+      float x[8];
 #pragma unroll
-  for (int kk = 0; kk < D / 2; ++kk) {
-    const int d = 2 * kk + hl;
-    qf[kk] = (qi < a.t_q && d < dh) ? f32blk::widen(qp[static_cast<int64_t>(qi) * a.lq.rs + d]) : 0.f;
-  }
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * nth + tid, mq = e / D, d = e % D;
+        const bool ok = e < kQS * D && qblk * kQS + mq < a.t_q && d < dh;
+        x[u] = f32blk::widen(qp[ok ? static_cast<int64_t>(qblk * kQS + mq) * a.lq.rs + d : 0]);
+        x[u] = ok ? x[u] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * nth + tid;
+        if (e < kQS * D) qs[(e / D) * P + e % D] = x[u];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < D / 2; ++kk) qf[kk] = qs[r32 * P + 2 * kk + hl];
+    __syncthreads();  // the tile loop reuses the buffer
+  };
   int kv_end = a.t_kv;
   if (a.causal) {
     const int last = min(qblk * kQS + kQS, a.t_q) - 1 + a.q_pos_offset;
@@ -166,6 +188,7 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
       };
       int j0 = j_first;
       if (j0 < kv_end) load(j0);
+      stage_q();
       for (; j0 < kv_end; j0 += j_step) {
         wave_sync();
 #pragma unroll
@@ -182,6 +205,7 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
     }
   }
   if (!(std::is_same<KT, float>::value && vec)) {
+    stage_q();
     for (int j0 = j_first; j0 < kv_end; j0 += j_step) {
       wave_sync();
 #pragma unroll 4
@@ -217,33 +241,61 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
     mo[kQS * R + kQS + r32] = l;
   }
   __syncthreads();
-  // Thread t merges element e = t, t + 64S, ... of the block's 32 x dh outputs.
-  // With ws > 1 it publishes (max, sum, unnormalized O) instead: rows of
-  // dh + 2 floats, [max, sum, O...], per (block, split).
+  // Per query row: the waves' weights e_w = exp(m_w - M) (0 for an empty
+  // wave) and the total sum L = sum_w e_w l_w, in wave order.
+  __shared__ float wts[kMaxSplit + 1][kQS];
+  auto mrow = [&](int w) { return reinterpret_cast<const float*>(&tl[w]); };
+  if (tid < kQS) {
+    float mw[kMaxSplit], M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMaxSplit; ++w) {
+      mw[w] = w < S ? mrow(w)[kQS * R + tid] : -INFINITY;
+      M = fmaxf(M, mw[w]);
+    }
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMaxSplit; ++w) {
+      const float ew = (mw[w] == -INFINITY) ? 0.f : expf(mw[w] - M);
+      wts[w][tid] = ew;
+      if (w < S) L += ew * mrow(w)[kQS * R + kQS + tid];
+    }
+    wts[kMaxSplit][tid] = L;
+    if (ws > 1) {
+      // Published rows: [max, sum, O...], dh + 2 floats per (block, split).
+      float* const mine = a.split_part + (static_cast<int64_t>(blk) * ws + wsplit) * kQS * (dh + 2);
+      st_agent(mine + tid * (dh + 2), M);
+      st_agent(mine + tid * (dh + 2) + 1, L);
+    }
+  }
+  __syncthreads();
+  // Output element e = (row e / dh, column e % dh): sum_w e_w O_w, eight
+  // elements per thread at a time with all their LDS reads in flight. With
+  // ws == 1 it is normalized and stored; otherwise published unnormalized.
   const int pitch = dh + 2;
   float* const mine = a.split_part + (static_cast<int64_t>(blk) * ws + wsplit) * kQS * pitch;
-  for (int e = tid; e < kQS * dh; e += 64 * S) {
-    const int mq = e / dh, d = e % dh;
-    const int oq = qblk * kQS + mq;
-    if (oq >= a.t_q) continue;
-    float M = -INFINITY;
-    for (int w = 0; w < S; ++w) M = fmaxf(M, reinterpret_cast<const float*>(&tl[w])[kQS * R + mq]);
-    float L = 0.f, acc = 0.f;
-    for (int w = 0; w < S; ++w) {
-      const float* t = reinterpret_cast<const float*>(&tl[w]);
-      const float mw = t[kQS * R + mq];
-      const float ew = (mw == -INFINITY) ? 0.f : expf(mw - M);
-      L += ew * t[kQS * R + kQS + mq];
-      acc += ew * t[mq * R + d];
+  const int ne = kQS * dh;
+  for (int e0 = 0; e0 < ne; e0 += 8 * nth) {
+    float acc[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = min(e0 + u * nth + tid, ne - 1), mq = e / dh, d = e % dh;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMaxSplit; ++w)
+        if (w < S) sum += wts[w][mq] * mrow(w)[mq * R + d];
+      acc[u] = sum;
     }
-    if (ws == 1) {
-      a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] =
-          acc * ((L > 0.f) ? 1.f / L : 0.f);
-    } else {
-      st_agent(mine + mq * pitch + 2 + d, acc);
-      if (d == 0) {
-        st_agent(mine + mq * pitch, M);
-        st_agent(mine + mq * pitch + 1, L);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * nth + tid, mq = e / dh, d = e % dh;
+      const int oq = qblk * kQS + mq;
+      if (e >= ne || oq >= a.t_q) continue;
+      if (ws == 1) {
+        const float L = wts[kMaxSplit][mq];
+        a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] =
+            acc[u] * ((L > 0.f) ? 1.f / L : 0.f);
+      } else {
+        st_agent(mine + mq * pitch + 2 + d, acc[u]);
       }
     }
   }
@@ -257,49 +309,75 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
              static_cast<unsigned>(ws - 1);
   __syncthreads();
   if (!merger) return;
-  // The fold: the rows' max and sum of every split into LDS (the tile
-  // buffers are free), then per row the weight of each split and the total
-  // sum, then each output element from its splits' partial sums, all of an
-  // element's loads in flight at once.
+  // The fold, in split order (bits independent of arrival order): the rows'
+  // max and sum of every split into LDS (the tile buffers are free), then per
+  // row the weight of each split and the total sum, then each output element
+  // from its splits' partial sums. Every round of loads is unrolled and
+  // unconditional (clamped indices), so all of a round is in flight at once.
   const float* const all = a.split_part + static_cast<int64_t>(blk) * ws * kQS * pitch;
   float* const sm = reinterpret_cast<float*>(&tl[0]);  // [kMaxWs][kQS] max, then weight
   float* const sl = sm + kMaxWs * kQS;                 // [kMaxWs][kQS] sum
   float* const sinv = sl + kMaxWs * kQS;               // [kQS] 1 / total sum, or 0
   static_assert(sizeof(Tiles<DB>) >= (2 * kMaxWs + 1) * kQS * sizeof(float), "fold fits");
-  for (int i = tid; i < ws * kQS; i += 64 * S) {
-    const float* const r = all + i * pitch;  // split i / kQS, row i % kQS
-    const float mx = ld_agent(r), lx = ld_agent(r + 1);
-    sm[i] = mx;
-    sl[i] = lx;
+  {
+    constexpr int kU = kMaxWs * kQS / 128;  // nth >= 128
+    const int nst = ws * kQS;
+    float mx[kU], lx[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const float* const r = all + min(u * nth + tid, nst - 1) * pitch;  // split i / kQS, row i % kQS
+      mx[u] = ld_agent(r);
+      lx[u] = ld_agent(r + 1);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = u * nth + tid;
+      if (i < nst) {
+        sm[i] = mx[u];
+        sl[i] = lx[u];
+      }
+    }
   }
   __syncthreads();
   if (tid < kQS) {
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < ws; ++s2) M = fmaxf(M, sm[s2 * kQS + tid]);
+    float ms[kMaxWs], M = -INFINITY;
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxWs; ++s2) {
+      ms[s2] = s2 < ws ? sm[s2 * kQS + tid] : -INFINITY;
+      M = fmaxf(M, ms[s2]);
+    }
     float L = 0.f;
-    for (int s2 = 0; s2 < ws; ++s2) {
-      const float ms = sm[s2 * kQS + tid];
-      const float es = (ms == -INFINITY) ? 0.f : expf(ms - M);
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxWs; ++s2) {
+      if (s2 >= ws) break;
+      const float es = (ms[s2] == -INFINITY) ? 0.f : expf(ms[s2] - M);
       sm[s2 * kQS + tid] = es;
       L += es * sl[s2 * kQS + tid];
     }
     sinv[tid] = (L > 0.f) ? 1.f / L : 0.f;
   }
   __syncthreads();
-  for (int e = tid; e < kQS * dh; e += 64 * S) {
-    const int mq = e / dh, d = e % dh;
-    const int oq = qblk * kQS + mq;
-    if (oq >= a.t_q) continue;
-    // Every slot loads (split 0's row past ws, weighted 0), so no branch
-    // stands between the loads.
-    float part[kMaxWs];
+  for (int e0 = 0; e0 < ne; e0 += 4 * nth) {
+    // Every slot loads (split 0's row past ws, left out of the sum).
+    float part[4][kMaxWs];
 #pragma unroll
-    for (int s2 = 0; s2 < kMaxWs; ++s2)
-      part[s2] = ld_agent(all + ((s2 < ws ? s2 : 0) * kQS + mq) * pitch + 2 + d);
-    float acc = 0.f;
+    for (int u = 0; u < 4; ++u) {
+      const int e = min(e0 + u * nth + tid, ne - 1), mq = e / dh, d = e % dh;
 #pragma unroll
-    for (int s2 = 0; s2 < kMaxWs; ++s2) acc += (s2 < ws ? sm[s2 * kQS + mq] : 0.f) * part[s2];
-    a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] = acc * sinv[mq];
+      for (int s2 = 0; s2 < kMaxWs; ++s2)
+        part[u][s2] = ld_agent(all + ((s2 < ws ? s2 : 0) * kQS + mq) * pitch + 2 + d);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = e0 + u * nth + tid, mq = e / dh, d = e % dh;
+      const int oq = qblk * kQS + mq;
+      if (e >= ne || oq >= a.t_q) continue;
+      float acc = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < kMaxWs; ++s2)
+        if (s2 < ws) acc += sm[s2 * kQS + mq] * part[u][s2];
+      a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] = acc * sinv[mq];
+    }
   }
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -315,16 +393,26 @@ int device_cus() {
   return cus;
 }
 
-// Workgroups per 32-query block of the key split: by default as many as fill
-// the CUs (at most kMaxWs, at most one per eight of the block's 32-key tiles,
-// so each wave keeps two tiles or more) where the blocks occupy fewer than
-// half the CUs; forced (a.force_f32_split == 5) at least two. 1: no split.
+// Waves per key-split workgroup: a.force_f32_split 2..4 forces that many.
+int ksplit_waves(const PrefillArgs& a) {
+  return a.force_f32_split >= 2 && a.force_f32_split <= 4 ? a.force_f32_split : kMaxSplit;
+}
+
+// Workgroups per 32-query block of the key split: by default, where the
+// blocks occupy fewer than half the CUs and one workgroup would give each
+// wave three tiles or more, as many as give every wave one of the block's
+// 32-key tiles (at most kMaxWs, at most the CUs per block); forced
+// (a.force_f32_split == 5) at least two. 1: no split.
 int ksplit_ways(const PrefillArgs& a, int64_t nws, int64_t cus) {
   const int forced = a.force_f32_split;
   if (forced != 5 && (forced != -1 || 2 * nws >= cus)) return 1;
   const int64_t tiles = (a.t_kv + f32blk::kN - 1) / f32blk::kN;
+  const int split = ksplit_waves(a);
+  // Under three tiles per wave the fold costs more than the split saves
+  // (64 queries x 6 heads over 188 keys: 18.5 against 16.4 us).
+  if (forced != 5 && tiles < 3 * split) return 1;
   int64_t ws = std::min<int64_t>({kMaxWs, cus / std::max<int64_t>(nws, 1),
-                                  std::max<int64_t>(1, tiles / kMaxSplit)});
+                                  std::max<int64_t>(1, (tiles + split - 1) / split)});
   if (forced == 5) ws = std::max<int64_t>(ws, 2);
   return static_cast<int>(ws);
 }
@@ -356,7 +444,7 @@ hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   // 1500 x 32 heads 279 against 347 us, 1500 x 320 heads 2447 against 2150 us.
   const int n_qs = (a.t_q + kQS - 1) / kQS;
   const int64_t nws = n_qs * bh;
-  const int split = forced >= 2 && forced <= 4 ? forced : kMaxSplit;
+  const int split = ksplit_waves(a);
   if (forced >= 1 || (forced != 0 && nwg <= 4 * static_cast<int64_t>(device_cus()))) {
     int ws = ksplit_ways(a, nws, device_cus());
     if (ws > 1 && !(a.split_part && a.split_counters &&
