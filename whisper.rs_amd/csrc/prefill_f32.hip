@@ -171,19 +171,20 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
 
   if constexpr (std::is_same<KT, float>::value) {
     if (vec) {
-      // f32 K/V rows of exactly D floats, 16-byte aligned: lane (key, half)
-      // loads half a K row and half a V row as float4s, one tile ahead of the
-      // tile it computes.
-      const int key = lane >> 1, c0 = (lane & 1) * (D / 2);
+      // f32 K/V rows of exactly D floats, 16-byte aligned: float4 f = lane +
+      // 64 i of the tile (key f / (D/4), column 4 (f % (D/4))), so each load
+      // instruction covers whole rows; one tile ahead of the tile computed.
+      // Keys past t_kv read the last key and are stored as 0.
+      constexpr int C4 = D / 4;
       f32x4 kr[D / 8], vr[D / 8];
       auto load = [&](int j0) {
-        const bool ok = j0 + key < a.t_kv;
-        const float* krow = kp + static_cast<int64_t>(j0 + key) * a.lk.rs + c0;
-        const float* vrow = vp + static_cast<int64_t>(j0 + key) * a.lv.rs + c0;
 #pragma unroll
         for (int i = 0; i < D / 8; ++i) {
-          kr[i] = ok ? *reinterpret_cast<const f32x4*>(krow + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
-          vr[i] = ok ? *reinterpret_cast<const f32x4*>(vrow + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+          const int f = lane + 64 * i, key = j0 + f / C4, c = 4 * (f % C4);
+          const int64_t row = min(key, a.t_kv - 1);
+          kr[i] = *reinterpret_cast<const f32x4*>(kp + row * a.lk.rs + c);
+          vr[i] = *reinterpret_cast<const f32x4*>(vp + row * a.lv.rs + c);
+          if (key >= a.t_kv) kr[i] = vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
       };
       int j0 = j_first;
@@ -192,12 +193,14 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
       for (; j0 < kv_end; j0 += j_step) {
         wave_sync();
 #pragma unroll
-        for (int i = 0; i < D / 8; ++i)
+        for (int i = 0; i < D / 8; ++i) {
+          const int f = lane + 64 * i, at = (f / C4) * P + 4 * (f % C4);
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            Ks[key * P + c0 + 4 * i + c] = kr[i][c];
-            Vs[key * P + c0 + 4 * i + c] = vr[i][c];
+            Ks[at + c] = kr[i][c];
+            Vs[at + c] = vr[i][c];
           }
+        }
         wave_sync();
         if (j0 + j_step < kv_end) load(j0 + j_step);
         tile(j0);
