@@ -201,3 +201,53 @@ def test_split_prefill_under_graph_capture(wrs, fresh_ctx):
         run()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"eager call after replay {rep} differs"
+
+
+def test_f32_workgroup_split_under_graph_capture(wrs, fresh_ctx):
+    # flash_attention_2's (64, 1500) x 6 heads shape in f32: each 32-query
+    # block's key tiles go to 12 workgroups folded through the same context
+    # scratch. Captured before any eager call the launch keeps one workgroup
+    # per block (no allocation); captured after, it replays the workgroup
+    # split bit-identically to eager calls, with eager work between replays.
+    note("f32 prefill (64, 1500) x 6 heads under graph capture")
+    ctx = fresh_ctx
+    H, TQ, TK = 6, 64, 1500
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    q = torch.randn((TQ, H * 64), generator=g, device="cuda")
+    k = torch.randn((TK, H * 64), generator=g, device="cuda")
+    v = torch.randn((TK, H * 64), generator=g, device="cuda")
+    lq, lk = wrs.token_major(TQ, H * 64, 64), wrs.token_major(TK, H * 64, 64)
+    out = torch.zeros((TQ, H * 64), device="cuda")
+
+    def run():
+        wrs.prefill(q, k, v, out, batch=1, n_heads=H, t_q=TQ, t_kv=TK, d_head=64,
+                    q_layout=lq, kv_layout=lk, out_layout=lq, ctx=ctx)
+
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g0):
+        ctx.use_torch_stream()
+        run()
+    ctx.use_torch_stream()
+    out.fill_(float("nan"))
+    g0.replay()
+    torch.cuda.synchronize()
+    before = out.clone()
+    run()  # outside capture: allocates the scratch, runs the workgroup split
+    torch.cuda.synchronize()
+    ref = out.clone()
+    assert torch.isfinite(ref).all()
+    assert maxerr(host(before), host(ref)) < 1e-5, "one and twelve workgroups per block disagree"
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        ctx.use_torch_stream()
+        run()
+    ctx.use_torch_stream()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        g1.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}: f32 workgroup split differs from eager"
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"eager call after replay {rep} differs"
