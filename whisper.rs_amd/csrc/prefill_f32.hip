@@ -322,6 +322,55 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
   float* const sl = sm + kMaxWs * kQS;                 // [kMaxWs][kQS] sum
   float* const sinv = sl + kMaxWs * kQS;               // [kQS] 1 / total sum, or 0
   static_assert(sizeof(Tiles<DB>) >= (2 * kMaxWs + 1) * kQS * sizeof(float), "fold fits");
+  // The first round carries the statistics and the first kF elements per
+  // thread; the barriers around the weights wait on LDS only, so those
+  // elements' loads stay in flight through them.
+  constexpr int kF = 8;
+  auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  float part[kF][kMaxWs];
+  // With d_head even, element pairs (d, d + 1) of a row are one 8-byte
+  // agent-scope load: a thread's kF elements are kF / 2 pairs.
+  const bool pairs = (dh & 1) == 0;
+  auto elem = [&](int e0, int u) {
+    return pairs ? e0 + 2 * ((u >> 1) * nth + tid) + (u & 1) : e0 + u * nth + tid;
+  };
+  auto fold_load = [&](int e0) {
+    if (pairs) {
+#pragma unroll
+      for (int u = 0; u < kF; u += 2) {
+        const int e = min(elem(e0, u), ne - 2), mq = e / dh, d = e % dh;
+#pragma unroll
+        for (int s2 = 0; s2 < kMaxWs; ++s2) {
+          const unsigned long long w = __hip_atomic_load(
+              reinterpret_cast<const unsigned long long*>(all + ((s2 < ws ? s2 : 0) * kQS + mq) * pitch + 2 + d),
+              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          part[u][s2] = __uint_as_float(static_cast<unsigned>(w));
+          part[u + 1][s2] = __uint_as_float(static_cast<unsigned>(w >> 32));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kF; ++u) {
+        const int e = min(elem(e0, u), ne - 1), mq = e / dh, d = e % dh;
+#pragma unroll
+        for (int s2 = 0; s2 < kMaxWs; ++s2)
+          part[u][s2] = ld_agent(all + ((s2 < ws ? s2 : 0) * kQS + mq) * pitch + 2 + d);
+      }
+    }
+  };
+  auto fold_store = [&](int e0) {
+#pragma unroll
+    for (int u = 0; u < kF; ++u) {
+      const int e = elem(e0, u), mq = e / dh, d = e % dh;
+      const int oq = qblk * kQS + mq;
+      if (e >= ne || oq >= a.t_q) continue;
+      float acc = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < kMaxWs; ++s2)
+        if (s2 < ws) acc += sm[s2 * kQS + mq] * part[u][s2];
+      a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] = acc * sinv[mq];
+    }
+  };
   {
     constexpr int kU = kMaxWs * kQS / 128;  // nth >= 128
     const int nst = ws * kQS;
@@ -332,6 +381,7 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
       mx[u] = ld_agent(r);
       lx[u] = ld_agent(r + 1);
     }
+    fold_load(0);
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int i = u * nth + tid;
@@ -341,7 +391,7 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < kQS) {
     float ms[kMaxWs], M = -INFINITY;
 #pragma unroll
@@ -352,35 +402,19 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
     float L = 0.f;
 #pragma unroll
     for (int s2 = 0; s2 < kMaxWs; ++s2) {
-      if (s2 >= ws) break;
       const float es = (ms[s2] == -INFINITY) ? 0.f : expf(ms[s2] - M);
-      sm[s2 * kQS + tid] = es;
-      L += es * sl[s2 * kQS + tid];
+      if (s2 < ws) {
+        sm[s2 * kQS + tid] = es;
+        L += es * sl[s2 * kQS + tid];
+      }
     }
     sinv[tid] = (L > 0.f) ? 1.f / L : 0.f;
   }
-  __syncthreads();
-  for (int e0 = 0; e0 < ne; e0 += 4 * nth) {
-    // Every slot loads (split 0's row past ws, left out of the sum).
-    float part[4][kMaxWs];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = min(e0 + u * nth + tid, ne - 1), mq = e / dh, d = e % dh;
-#pragma unroll
-      for (int s2 = 0; s2 < kMaxWs; ++s2)
-        part[u][s2] = ld_agent(all + ((s2 < ws ? s2 : 0) * kQS + mq) * pitch + 2 + d);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = e0 + u * nth + tid, mq = e / dh, d = e % dh;
-      const int oq = qblk * kQS + mq;
-      if (e >= ne || oq >= a.t_q) continue;
-      float acc = 0.f;
-#pragma unroll
-      for (int s2 = 0; s2 < kMaxWs; ++s2)
-        if (s2 < ws) acc += sm[s2 * kQS + mq] * part[u][s2];
-      a.o[b * a.lo.bs + h * a.lo.hs + static_cast<int64_t>(oq) * a.lo.rs + d] = acc * sinv[mq];
-    }
+  lds_barrier();
+  fold_store(0);
+  for (int e0 = kF * nth; e0 < ne; e0 += kF * nth) {
+    fold_load(e0);
+    fold_store(e0);
   }
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
