@@ -78,10 +78,12 @@ def test_host_slice_kat(wrs, orc, ctx, t_q, t_kv, h, dh, causal, f32_schedule):
     assert maxerr(out.reshape(t_q, d_model), ref) <= TOL32
 
 
-@pytest.mark.parametrize("dh,causal", [(32, False), (96, True), (128, False), (128, True)])
+@pytest.mark.parametrize("dh,causal", [(32, False), (96, True), (128, False), (128, True),
+                                       (33, False), (75, True)])
 def test_host_slice_head_sizes(wrs, orc, ctx, dh, causal, f32_schedule):
     # d_head 32, 96 and 128: one, three and four 32-wide d blocks, rows of exactly
-    # that many floats (the key split's float4 row loads)
+    # that many floats (the key split's float4 row loads); 33 and 75: odd widths
+    # (element loads, and the workgroup split's fold one float at a time)
     t_q, t_kv, h = 70, 133, 3
     d_model = h * dh
     note(f"host-slice flash_attention_2 d_head={dh} causal={causal}")
