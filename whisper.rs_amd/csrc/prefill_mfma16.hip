@@ -208,14 +208,7 @@ template <int QB>
 constexpr int kSlots() {
   return 8 * QB;
 }
-#ifndef WRS_PIPE_A
-#define WRS_PIPE_A 2
-#define WRS_PIPE_B 3
-#endif
-#ifndef WRS_QK_SEQ
-#define WRS_QK_SEQ 0
-#endif
-constexpr int pipe_fma_slot(int u) { return (WRS_PIPE_A * u) / WRS_PIPE_B; }
+constexpr int pipe_fma_slot(int u) { return (2 * u) / 3; }
 constexpr int pipe_rowsum_slot(int jb) { return pipe_fma_slot(8 * jb + 7) + 3; }
 // Program order must respect the data flow: the pack of unit u overwrites
 // register pb[u/8][(u/4)%2] after the P V MFMAs of the previous step have read
@@ -608,7 +601,7 @@ __global__ __launch_bounds__(64 * QW * KH, 2 / KH) void fa2_prefill_d64(
           o[jb][hf] = mfma_f16(u32x4{v0.x, v0.y, v1.x, v1.y}, pb[jb][k2], o[jb][hf]);
         } else {
           const int qn = n - 4 * kQB;
-          const int dk = WRS_QK_SEQ ? qn % 4 : qn / kQB, jb = WRS_QK_SEQ ? qn / 4 : qn % kQB;
+          const int dk = qn / kQB, jb = qn % kQB;
           s_next[jb] = Elem<T>::mfma(ka[dk], qf[jb][dk], dk == 0 ? f32x16{} : s_next[jb]);
         }
 #pragma unroll
