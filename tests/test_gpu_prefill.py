@@ -628,3 +628,38 @@ def test_prefill_random_shapes(wrs, ctx, B, H, t_q, t_kv, causal, offset, dtype,
     for b in range(B):
         ref = attention_f64(q[b], k[b], v[b], t_q, t_kv, H, dm, causal=causal, q_offset=offset)
         assert maxerr(got[b], ref) <= TOL16, b
+
+
+def _random_f32_shapes(n=8, seed=0xF32_5EED):
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for _ in range(n):
+        causal = bool(rng.integers(2))
+        shapes.append((int(rng.integers(1, 3)), int(rng.integers(1, 5)), int(rng.integers(1, 300)),
+                       int(rng.integers(1, 1600)), causal,
+                       int(rng.integers(0, 200)) if causal else 0,
+                       int(rng.choice([64, 64, 40, 96]))))
+    return shapes
+
+
+@pytest.mark.parametrize("B,H,t_q,t_kv,causal,offset,dh", _random_f32_shapes())
+def test_prefill_random_shapes_f32(wrs, ctx, B, H, t_q, t_kv, causal, offset, dh, f32_schedule):
+    # Seeded random f32 batch, head, length, width, mask and offset combinations
+    # under every f32 schedule (the workgroup split included), against the
+    # float64 reference at the f32 bar.
+    dm = H * dh
+    note(f"device prefill f32 B={B} H={H} t_q={t_q} t_kv={t_kv} dh={dh} causal={causal} "
+         f"offset={offset}")
+    rng = np.random.default_rng(t_q * 7919 + t_kv)
+    q = rng.standard_normal((B, t_q, dm), dtype=np.float32)
+    k = rng.standard_normal((B, t_kv, dm), dtype=np.float32)
+    v = rng.standard_normal((B, t_kv, dm), dtype=np.float32)
+    out = torch.full((B, t_q, dm), float("nan"), dtype=torch.float32, device="cuda")
+    lq, lk = wrs.token_major(t_q, dm, dh), wrs.token_major(t_kv, dm, dh)
+    wrs.prefill(dev(q, torch.float32), dev(k, torch.float32), dev(v, torch.float32), out,
+                batch=B, n_heads=H, t_q=t_q, t_kv=t_kv, d_head=dh, q_layout=lq, kv_layout=lk,
+                out_layout=lq, causal=causal, q_pos_offset=offset, ctx=ctx)
+    got = host(out)
+    for b in range(B):
+        ref = attention_f64(q[b], k[b], v[b], t_q, t_kv, H, dm, causal=causal, q_offset=offset)
+        assert maxerr(got[b], ref) <= TOL32, b
