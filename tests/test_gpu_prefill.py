@@ -46,11 +46,11 @@ def schedule(request, ctx):
 @pytest.fixture(params=[-1, 0, 1, 3, 5],
                 ids=["f32default", "f32block", "f32ksplit", "f32ksplit3", "f32ksplitws"])
 def f32_schedule(request, ctx):
-    """The schedules of the f32 kernel on the same shapes: grids of up to four
-    128-query blocks per CU normally take the key-split workgroups (32 queries,
-    key tiles interleaved over four waves; three when forced to 3), larger ones
-    128-query blocks; grids of fewer 32-query blocks than half the CUs spread
-    each block over several key-split workgroups (forced: 5)."""
+    """The schedules of the f32 kernel on the same shapes: the key-split
+    workgroups by default (32 queries, key tiles interleaved over four waves;
+    three when forced to 3), 128-query blocks when forced (0); grids of fewer
+    32-query blocks than half the CUs spread each block over several key-split
+    workgroups (forced: 5)."""
     ctx.set_schedule(f32_split=request.param)
     yield request.param
     ctx.set_schedule()

@@ -24,7 +24,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, in
   __shared__ Tiles<DB> tl;
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = lid / n_qblk;
-  fa2_block<QT, KT, DB>(a, (lid % n_qblk) * f32blk::kM, bh % a.n_heads, bh / a.n_heads, tl);
+  fa2_block<QT, KT, DB, 4, true>(a, (lid % n_qblk) * f32blk::kM, bh % a.n_heads, bh / a.n_heads, tl);
 }
 
 // Small grids of 128-query blocks (whisper-tiny's encoder: 12 blocks x 6
@@ -41,6 +41,11 @@ __global__ __launch_bounds__(kThreads, 1) void fa2_prefill_f32(PrefillArgs a, in
 // with agent-scope stores, and the last of the block's workgroups to count in
 // folds them in split order (bits independent of arrival order), re-arms the
 // block's counter and writes the rows.
+// exp(x) as the hardware's exp2 of x log2(e). For the softmax's x <= 0 the
+// rounding of the product moves a weight e^x by at most |x| e^x 2^-24, below
+// 2.2e-8 absolute; libm's expf is a ~10-instruction range reduction.
+__device__ inline float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
+
 constexpr int kQS = 32;       // queries per k-split workgroup
 constexpr int kMaxSplit = 4;  // waves per k-split workgroup, at most
 constexpr int kMaxWs = 16;    // workgroups per block, at most
@@ -128,32 +133,37 @@ __global__ __launch_bounds__(64 * kMaxSplit, DB <= 2 ? 2 : 1) void fa2_prefill_f
   };
   // The same per-tile arithmetic as fa2_block (attention.rs:141-222).
   auto tile = [&](int j0) {
-    // Four independent accumulator chains over d: with one wave per SIMD a
+    // Two independent accumulator chains over d: with one wave per SIMD a
     // single chain would wait out every MFMA's latency.
-    f32x16 sp[4] = {};
+    f32x16 sp[2] = {};
 #pragma unroll
     for (int kk = 0; kk < D / 2; ++kk)
-      sp[kk & 3] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk],
-                                                         sp[kk & 3], 0, 0, 0);
-    f32x16 sc = (sp[0] + sp[1]) + (sp[2] + sp[3]);
+      sp[kk & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk],
+                                                         sp[kk & 1], 0, 0, 0);
+    f32x16 sc = sp[0] + sp[1];
+    // Tiles wholly inside the key range (and, with the causal mask, at or
+    // below the block's first query position) need no masking.
+    const bool whole = j0 + kN <= a.t_kv && (!a.causal || j0 + kN - 1 <= qblk * kQS + a.q_pos_offset);
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = j0 + 8 * (i >> 2) + 4 * hl + (i & 3);
       float x = a.scale * sc[i];
-      if (key >= a.t_kv || (a.causal && key > qpos)) x = -INFINITY;
+      if (!whole) {
+        const int key = j0 + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (key >= a.t_kv || (a.causal && key > qpos)) x = -INFINITY;
+      }
       sc[i] = x;
       mx = fmaxf(mx, x);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx);
-    const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
+    const float alpha = (m == -INFINITY) ? 0.f : fexp(m - m_new);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     m = m_new;
     float ls = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      sc[i] = expf(sc[i] - m_use);
+      sc[i] = fexp(sc[i] - m_use);
       ls += sc[i];
     }
     l = l * alpha + ls;
@@ -474,15 +484,14 @@ hipError_t launch_typed(const PrefillArgs& a, hipStream_t s) {
   // a.force_f32_split: 0 forces 128-query blocks, 1 the key split, 2..4 the
   // key split over that many waves, 5 the key split over several workgroups.
   const int forced = a.force_f32_split;
-  // The key split, four waves per 32-query block, up to 4 blocks of 128
-  // queries per CU; beyond that the 128-query blocks, whose four waves share
-  // every tile load, have waves enough. Measured (f32, d_head 64, one window):
-  // 1500 x 6 heads 94 against 208 us, 4096 x 6 heads 341 against 711 us,
-  // 1500 x 32 heads 279 against 347 us, 1500 x 320 heads 2447 against 2150 us.
+  // The key split, four waves per 32-query block, at every grid size.
+  // Measured against the 128-query blocks (f32, d_head 64, 1500 queries and
+  // keys): 6 heads 75 against 168 us, 32 heads 213 against 278 us, 128 heads
+  // 790 against 797 us, 320 heads 1935 against 1972 us.
   const int n_qs = (a.t_q + kQS - 1) / kQS;
   const int64_t nws = n_qs * bh;
   const int split = ksplit_waves(a);
-  if (forced >= 1 || (forced != 0 && nwg <= 4 * static_cast<int64_t>(device_cus()))) {
+  if (forced != 0) {
     int ws = ksplit_ways(a, nws, device_cus());
     if (ws > 1 && !(a.split_part && a.split_counters &&
                     ksplit_floats(a, nws, ws) <= static_cast<int64_t>(a.split_part_floats) &&
@@ -522,10 +531,7 @@ void prefill_f32_scratch(const PrefillArgs& a, size_t* part_floats, size_t* coun
   *part_floats = *counter_words = 0;
   const int64_t nws = blocks32(a);
   if (a.t_q <= 0 || nws <= 0 || a.force_f32_split == 0) return;
-  const int64_t nwg = ((a.t_q + kM - 1) / kM) * static_cast<int64_t>(a.n_heads) * a.batch;
-  const int64_t cus = device_cus();
-  if (a.force_f32_split < 1 && nwg > 4 * cus) return;  // 128-query blocks
-  const int ws = ksplit_ways(a, nws, cus);
+  const int ws = ksplit_ways(a, nws, device_cus());
   if (ws == 1) return;
   *part_floats = static_cast<size_t>(ksplit_floats(a, nws, ws));
   *counter_words = static_cast<size_t>(ksplit_words(nws));

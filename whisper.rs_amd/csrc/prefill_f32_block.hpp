@@ -42,7 +42,11 @@ struct Tiles {
 // entry b, run by NW waves (4 in the f32 kernel: a 128-query block), rows at
 // or past a.t_q left alone. DB: number of 32-wide blocks covering d_head
 // (<= 32*DB).
-template <typename QT, typename KT, int DB, int NW = 4>
+// kFast (the f32 kernel's 128-query blocks): the next tile's rows load into
+// registers during the current tile, score chains over d are two, exp is the
+// hardware exp2 of x log2(e), and tiles wholly inside the key range skip the
+// mask. K1's bf16 recompute keeps the plain form.
+template <typename QT, typename KT, int DB, int NW = 4, bool kFast = false>
 __device__ inline void fa2_block(const PrefillArgs& a, int q_begin, int h, int b, Tiles<DB>& tl) {
   constexpr int D = 32 * DB;
   constexpr int P = Tiles<DB>::P;
@@ -79,43 +83,98 @@ __device__ inline void fa2_block(const PrefillArgs& a, int q_begin, int h, int b
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
   float m = -INFINITY, l = 0.f;
 
+  // kFast: thread tid holds elements tid + 64 NW u of the next tile.
+  constexpr int kE = (kN * D + 64 * NW - 1) / (64 * NW);
+  float kr[kFast ? kE : 1], vr[kFast ? kE : 1];
+  auto load = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < kE; ++u) {
+      const int e = tid + 64 * NW * u, key = e / D, d = e % D;
+      const bool ok = e < kN * D && j0 + key < a.t_kv && d < dh;
+      const int64_t row = min(j0 + key, a.t_kv - 1);
+      const int col = min(d, dh - 1);
+      kr[u] = widen(kp[row * a.lk.rs + col]);
+      vr[u] = widen(vp[row * a.lv.rs + col]);
+      if (!ok) kr[u] = vr[u] = 0.f;
+    }
+  };
+  if constexpr (kFast) {
+    if (kv_end > 0) load(0);
+  }
+  auto ex = [](float x) {
+    if constexpr (kFast)
+      return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f);
+    else
+      return expf(x);
+  };
+
   for (int j0 = 0; j0 < kv_end; j0 += kN) {
     __syncthreads();
-    for (int e = tid; e < kN * D; e += 64 * NW) {
-      const int key = e / D, d = e % D;
-      float kv = 0.f, vv = 0.f;
-      if (j0 + key < a.t_kv && d < dh) {
-        kv = widen(kp[static_cast<int64_t>(j0 + key) * a.lk.rs + d]);
-        vv = widen(vp[static_cast<int64_t>(j0 + key) * a.lv.rs + d]);
+    if constexpr (kFast) {
+#pragma unroll
+      for (int u = 0; u < kE; ++u) {
+        const int e = tid + 64 * NW * u;
+        if (e < kN * D) {
+          Ks[(e / D) * P + e % D] = kr[u];
+          Vs[(e / D) * P + e % D] = vr[u];
+        }
       }
-      Ks[key * P + d] = kv;
-      Vs[key * P + d] = vv;
+      __syncthreads();
+      if (j0 + kN < kv_end) load(j0 + kN);
+    } else {
+      for (int e = tid; e < kN * D; e += 64 * NW) {
+        const int key = e / D, d = e % D;
+        float kv = 0.f, vv = 0.f;
+        if (j0 + key < a.t_kv && d < dh) {
+          kv = widen(kp[static_cast<int64_t>(j0 + key) * a.lk.rs + d]);
+          vv = widen(vp[static_cast<int64_t>(j0 + key) * a.lv.rs + d]);
+        }
+        Ks[key * P + d] = kv;
+        Vs[key * P + d] = vv;
+      }
+      __syncthreads();
     }
-    __syncthreads();
 
     f32x16 s = {};
+    if constexpr (kFast) {
+      f32x16 s1 = {};
 #pragma unroll
-    for (int kk = 0; kk < D / 2; ++kk)
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk], s, 0, 0, 0);
+      for (int kk = 0; kk < D / 2; kk += 2) {
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk], s, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + 2 + hl], qf[kk + 1], s1,
+                                                  0, 0, 0);
+      }
+      s += s1;
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < D / 2; ++kk)
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[r32 * P + 2 * kk + hl], qf[kk], s, 0, 0, 0);
+    }
 
+    // Tiles wholly inside the key range (and, with the causal mask, at or
+    // below the block's first query position) need no masking.
+    const bool whole = kFast && j0 + kN <= a.t_kv &&
+                       (!a.causal || j0 + kN - 1 <= q_begin + a.q_pos_offset);
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = j0 + 8 * (i >> 2) + 4 * hl + (i & 3);
       float x = a.scale * s[i];
-      if (key >= a.t_kv || (a.causal && key > qpos)) x = -INFINITY;
+      if (!whole) {
+        const int key = j0 + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (key >= a.t_kv || (a.causal && key > qpos)) x = -INFINITY;
+      }
       s[i] = x;
       mx = fmaxf(mx, x);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx);
-    const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
+    const float alpha = (m == -INFINITY) ? 0.f : ex(m - m_new);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     m = m_new;
     float ls = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[i] = expf(s[i] - m_use);
+      s[i] = ex(s[i] - m_use);
       ls += s[i];
     }
     l = l * alpha + ls;
