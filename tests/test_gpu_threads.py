@@ -6,7 +6,10 @@ attention from OS threads in whisper_full_parallel
 Four host threads each own a context (and its stream) and, at the same time,
 run synchronous host-slice calls (flash_attention_2 on f32 host slices) and
 asynchronous device-resident calls (an f16 encoder prefill and a beam-5
-cross-attention decode over their own arena). Every result is compared with
+cross-attention decode over their own arena). Threads 0 and 2 take the shapes
+whose work is merged through the context's scratch: the 64-query host slice
+over 1500 keys (each block's tiles over twelve workgroups) and one
+whisper-base window (each 128-query block over two workgroups). Every result is compared with
 the oracle's, computed beforehand on the same inputs; a thread stops at its
 first failure and the test reports it. ctypes releases the GIL for the
 duration of each library call, so the calls do overlap in the library.
@@ -37,16 +40,18 @@ def _oracle_fa2(orc, q, k, v, t_q, t_kv, h, dm, causal=False):
 def _case(orc, W, i):
     """Inputs and oracle results of thread i (distinct seeds per thread)."""
     c = {}
-    # host slice, f32: (100, 137) keys, 3 heads of 64, causal on odd threads
-    t_q, t_kv, h = 100, 137, 3
+    # host slice, f32: (100, 137) keys, 3 heads of 64, causal, on odd threads;
+    # (64, 1500), 6 heads, on even ones
+    t_q, t_kv, h = (100, 137, 3) if i & 1 else (64, 1500, 6)
     dm = h * 64
     c["hs"] = dict(q=W.normal((t_q, dm), 700 + 10 * i), k=W.normal((t_kv, dm), 701 + 10 * i),
                    v=W.normal((t_kv, dm), 702 + 10 * i), t_q=t_q, t_kv=t_kv, h=h, dm=dm,
                    causal=bool(i & 1))
     d = c["hs"]
     d["ref"] = _oracle_fa2(orc, d["q"], d["k"], d["v"], t_q, t_kv, h, dm, d["causal"])
-    # device-resident prefill, f16: 2 windows x 4 heads x 300 frames
-    B, H, T = 2, 4, 300
+    # device-resident prefill, f16: 2 windows x 4 heads x 300 frames on odd
+    # threads, one whisper-base window (8 heads x 1500 frames) on even ones
+    B, H, T = (2, 4, 300) if i & 1 else (1, 8, 1500)
     dmp = H * 64
     q = W.normal((B, T, dmp), 800 + 10 * i, storage="f16")
     k = W.normal((B, T, dmp), 801 + 10 * i, storage="f16")
