@@ -128,7 +128,12 @@ __device__ inline float sum_x16_x32(float x) {
 // kDecodeChunk) in general, 8 waves of two (kDecodeChunkLong = 256 keys) when
 // that covers the whole sequence, which then needs no split-K merge. Tile t of
 // wave w covers keys 128t + 16w.. of the workgroup's chunk.
-template <int R, int kMWaves, int kTiles>
+// kDS == 4 (launches of one split per plane): the plane's 64 output columns
+// are dealt to 4 workgroups, each reading all of K (the scores and softmax,
+// repeated in each) but only its 16 columns of V, and writing those columns.
+// One-split self-decode planes are bound by how fast one CU takes in its
+// rows; this spreads them over 4 CUs of one XCD without a merge.
+template <int R, int kMWaves, int kTiles, int kDS = 1>
 __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   static_assert(kMWaves >= kMaxRowsPerGroup, "one merging wave per query row");
   static_assert(kMWaves == 8, "tile t of wave w starts at key 128t + 16w");
@@ -137,7 +142,14 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   __shared__ float wm[kMWaves][8], wl[kMWaves][8];
   __shared__ int last_flag;
 
-  const int split = blockIdx.x, h = blockIdx.y, g = blockIdx.z;
+  static_assert(kDS == 1 || kDS == 4, "whole or quarter rows of V");
+  // kDS > 1: a 1-D grid of planes x parts, remapped so that a plane's parts
+  // are neighbours on one XCD (their K reads meet in its L2).
+  const int lid = kDS > 1 ? xcd_remap(blockIdx.x, gridDim.x) : 0;
+  const int split = kDS > 1 ? 0 : blockIdx.x;
+  const int h = kDS > 1 ? (lid / kDS) % a.n_heads : blockIdx.y;
+  const int g = kDS > 1 ? (lid / kDS) / a.n_heads : blockIdx.z;
+  const int dpart = kDS > 1 ? lid % kDS : 0;  // columns [64/kDS dpart, 64/kDS (dpart+1))
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   constexpr int rows = R;  // == a.rows_per_group
   const int len = a.len[g];
@@ -187,13 +199,24 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.v + plane), 0, range, kRawBuffer);
   u32x4 kx0[kTiles], kx1[kTiles], vx0[kTiles], vx1[kTiles];
+  // kDS == 4: vx0 holds the V half with the workgroup's 16 columns (d 32 hv +
+  // 8 kg ..); lanes whose 8 columns lie outside them read zero through an
+  // offset past the buffer's range (no memory access).
+  const int hv = dpart >> 1;
+  const bool vneed = (kg >> 1) == (dpart & 1);
 #pragma unroll
   for (int tt = 0; tt < kTiles; ++tt) {
     const uint32_t voff = static_cast<uint32_t>(kbase + 128 * tt + col) * 128u + 16u * kg;
     kx0[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff, 0, 0));
     kx1[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff + 64, 0, 0));
-    vx0[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, 0, 0));
-    vx1[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 64, 0, 0));
+    if constexpr (kDS == 1) {
+      vx0[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, 0, 0));
+      vx1[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 64, 0, 0));
+    } else {
+      const uint32_t vo = vneed ? voff + 64u * hv : 0xFFFFFFF0u;
+      vx0[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo, 0, 0));
+      vx1[tt] = vx0[tt];
+    }
   }
   // Every load above is issued before any of them is waited on: the q
   // arithmetic below depends on a value defined after them.
@@ -294,12 +317,15 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   }
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
+    // 16-column tile dt belongs to part dt / (4 / kDS).
+    if (kDS > 1 && dt / (4 / kDS) != dpart) continue;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 o = z;
 #pragma unroll
     for (int tt = 0; tt < kTiles; ++tt) {
       const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          __builtin_bit_cast(f16x8, dt < 2 ? vx0[tt] : vx1[tt]), (dt & 1) ? e1 : e0, z, 0, 0, 0);
+          __builtin_bit_cast(f16x8, dt < 2 || kDS > 1 ? vx0[tt] : vx1[tt]), (dt & 1) ? e1 : e0, z,
+          0, 0, 0);
       const f16x4 vb = __builtin_convertvector(t, f16x4);
       o = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[tt], vb, o, 0, 0, 0);
     }
@@ -315,8 +341,8 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   // Thread (row qr, d qd) of the first rows*64 threads folds the waves'
   // partials (log-sum-exp, exp2 domain); rows r and r+8 are the high and low
   // parts of the weights.
-  const int qr = tid >> 6, qd = tid & 63;
-  const bool own = qr < rows;
+  const int qr = tid >> 6, qd = kDS > 1 ? (64 / kDS) * dpart + (tid & 63) : tid & 63;
+  const bool own = qr < rows && (kDS == 1 || (tid & 63) < 64 / kDS);
   float pv = 0.f, M = -INFINITY, Lsum = 0.f;
   if (own) {
 #pragma unroll
@@ -333,7 +359,7 @@ __global__ __launch_bounds__(64 * kMWaves) void decode_f16(DecodeArgs a) {
   if (a.n_splits == 1) {
     if (own) {
       a.o[static_cast<int64_t>(g * rows + qr) * a.o_rs + h * 64 + qd] = Lsum > 0.f ? pv * (1.f / Lsum) : 0.f;
-      if (a.lse && qd == 0) store_lse(a, g * rows + qr, h, M, Lsum);
+      if (a.lse && qd == 0) store_lse(a, g * rows + qr, h, M, Lsum);  // part 0 only
     }
     return;
   }
@@ -564,11 +590,32 @@ size_t decode_counter_words(int n_groups, int n_heads) {
   return static_cast<size_t>(n_groups) * n_heads * kCounterStride;
 }
 
+// CUs of the current device, read once.
+int decode_cus() {
+  static const int cus = [] {
+    int dev = 0, n = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+      (void)hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    return n;
+  }();
+  return cus;
+}
+
 hipError_t launch_decode_f16(const DecodeArgs& a, hipStream_t s) {
   if (a.n_groups <= 0 || a.n_splits <= 0) return hipSuccess;
   if (a.chunk != kDecodeChunk && a.chunk != kDecodeChunkLong) return hipErrorInvalidValue;
   static_assert(kDecodeChunk == 128 && kDecodeChunkLong == 256, "8 waves of one or two tiles");
   const bool lng = a.chunk == kDecodeChunkLong;
+  const int64_t planes = static_cast<int64_t>(a.n_groups) * a.n_heads;
+  if (a.rows_per_group == 1 && lng && a.n_splits == 1 && 4 * planes <= decode_cus()) {
+    // One-row planes of 129-256 keys (self decode) on a quarter of the CUs or
+    // fewer: their V columns over 4 workgroups each. Same-box A/B, whisper-small
+    // 5 slots x 12 heads: 4.69 against 4.78 us at 224 keys, 4.87 against
+    // 4.98 at 256; halves, or quarters at 128 keys and below, were slower.
+    const dim3 grid(static_cast<unsigned>(4 * planes)), block(512);
+    hipLaunchKernelGGL((decode_f16<1, 8, 2, 4>), grid, block, 0, s, a);
+    return hipGetLastError();
+  }
   const dim3 grid(a.n_splits, a.n_heads, a.n_groups), block(512);
 #define WRS_DEC(R)                                                          \
   if (lng)                                                                  \
